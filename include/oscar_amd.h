@@ -1,0 +1,88 @@
+/* oscar_amd.h — C ABI of the MI355X (gfx950) OSCAR INT2 KV-cache kernels.
+ *
+ * Library: oscar_amd/_oscar_hip.so (built by oscar_amd/csrc/build.py).
+ *
+ * Conventions for every entry point:
+ *   - all tensor arguments are raw device pointers; sizes are element counts,
+ *     strides of the paged caches are in BYTES (the reference addresses the
+ *     caches through their uint8 view);
+ *   - work is enqueued on `stream` and never synchronised; the return value
+ *     is an oscar_status (0 = success, negative = error, nothing enqueued);
+ *   - head_size must be 256 (kernels are written for D = 256);
+ *   - caches are the engine's paged tensors (pages, block_size, Hk, W) with a
+ *     per-head slot width W >= 96 bytes; the K slot holds 8 meta bytes at
+ *     +0, pad at +8..31 (never written) and the K codes at +32; the V slot
+ *     holds the V codes at +0.
+ */
+#ifndef OSCAR_AMD_H
+#define OSCAR_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* oscar_stream_t; /* == hipStream_t */
+
+enum oscar_status {
+  OSCAR_OK = 0,
+  OSCAR_ERR_INVALID_ARGUMENT = -1,
+  OSCAR_ERR_UNSUPPORTED_HEAD_DIM = -2,
+  OSCAR_ERR_WORKSPACE_TOO_SMALL = -3,
+  OSCAR_ERR_LAUNCH = -4,
+  OSCAR_ERR_UNSUPPORTED_GEOMETRY = -5,
+};
+
+/* ---------------------------------------------------------------- rotation
+ * Prepare the MFMA operand of one orthogonal rotation R [D][D] fp32
+ * (x_rot = x @ R).  Replaces the reference's per-call fp32 matmul operand
+ * (oscar_ascend/backend.py:130 `torch.matmul(x.float(), R)`, rotations cached
+ * per layer at backend.py:228-236).  `operand` must hold
+ * oscar_rotation_operand_bytes(D) bytes (bf16 hi + lo split, permuted).
+ */
+size_t oscar_rotation_operand_bytes(int32_t head_size);
+int oscar_rotation_operand(const float* rotation, void* operand, int32_t head_size,
+                           oscar_stream_t stream);
+
+/* ---------------------------------------------------------------- quantize-write
+ * Fused rotate + clip + INT2 quantize + pack + paged-slot write.
+ * Replaces do_kv_cache_update's _rotate_clip + oscar_store_triton
+ * (oscar_ascend/backend.py:150-189, oscar_ascend/kernels/store_kernel.py:247-279).
+ *   key_bf16, value_bf16: [num_tokens][token_stride] bf16, the Hk*D features of
+ *                         each token first (token_stride in elements);
+ *   rot_*_operand:        from oscar_rotation_operand;
+ *   slot_mapping:         [num_tokens] int64, slot < 0 skipped (as are slots
+ *                         at or beyond num_pages * block_size);
+ *   clip_index_*:         sorted-|x| index of the clip threshold
+ *                         (min(int(ratio * D), D - 1)), or -1 for no clip.
+ */
+int oscar_quant_write(const void* key_bf16, const void* value_bf16, int64_t num_tokens,
+                      int32_t num_kv_heads, int32_t head_size, int64_t token_stride,
+                      const void* rot_k_operand, const void* rot_v_operand,
+                      const int64_t* slot_mapping, void* k_cache, void* v_cache,
+                      int32_t block_size, int64_t num_pages, int64_t k_stride_page,
+                      int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
+                      int64_t v_stride_token, int64_t v_stride_head, int32_t clip_index_k,
+                      int32_t clip_index_v, oscar_stream_t stream);
+
+/* Same as oscar_quant_write for input that is already rotated (fp32,
+ * [num_tokens][token_stride]); bytes are bit-exact with the reference store
+ * given identical rotated input.  Replaces the clip half of _rotate_clip plus
+ * oscar_store_ref / oscar_store_triton (backend.py:131-147,
+ * store_kernel.py:54-102, 247-279).
+ */
+int oscar_quant_write_prerotated(const float* k_rot, const float* v_rot, int64_t num_tokens,
+                                 int32_t num_kv_heads, int32_t head_size, int64_t token_stride,
+                                 const int64_t* slot_mapping, void* k_cache, void* v_cache,
+                                 int32_t block_size, int64_t num_pages, int64_t k_stride_page,
+                                 int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
+                                 int64_t v_stride_token, int64_t v_stride_head,
+                                 int32_t clip_index_k, int32_t clip_index_v, oscar_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OSCAR_AMD_H */

@@ -1,0 +1,385 @@
+// Fused rotate + sort-clip + INT2 quantize + 4-codes-per-byte pack + paged
+// slot write (gfx950).
+//
+// Work layout: one wavefront owns 32 tokens of one (kv-head, K-or-V) side.
+// Lane l holds token (l & 31), features 128*(l >> 5) .. +127 of that token in
+// 128 fp32 registers, so every per-vector reduction is lane-local plus one
+// exchange with lane l ^ 32.  That is exactly the fp32 accumulator layout of
+// a 32x32 MFMA tile whose columns are tokens, which the fused entry point
+// uses for the 256x256 rotation (bf16 hi + lo split of R, two passes).
+//
+// Quantization is bit-exact with the reference's fp32 formula
+//   q = clamp(floor((x - zero) / scale + 0.5), 0, 3)
+// without a per-value divide: with t = fl(x - zero), q >= n holds exactly when
+// t >= T_n, where T_n is the smallest float at or above scale * c_n (c_1 just
+// below 0.5, c_2 just below 1.5, c_3 just below 2.5; the offsets encode the
+// round-to-nearest-even ties of the divide and of the +0.5), computed once
+// per vector in fp64 (exact: scale has 11 significant bits).
+#include "oscar_common.h"
+
+namespace oscar {
+namespace {
+
+constexpr int kPerLane = kHeadDim / 2;      // 128 values of one vector per lane
+constexpr int kTokPerWave = 32;
+
+struct CacheArgs {
+  uint8_t* k_cache;
+  uint8_t* v_cache;
+  int64_t k_page, k_tok, k_head;     // byte strides
+  int64_t v_page, v_tok, v_head;
+  int32_t block_size;
+  int64_t num_slots;                 // pages * block_size; larger slots are skipped
+};
+
+// Exact value of ascending-sorted |x| at index `idx` over the 256 values held
+// by this lane and its partner (l ^ 32).  Bitwise radix select on the IEEE
+// bit pattern: for non-negative finite floats, float order equals bit order.
+__device__ float select_abs_rank(const float (&v)[kPerLane], int idx) {
+  uint32_t prefix = 0;
+#pragma unroll 1
+  for (int bit = 30; bit >= 0; --bit) {
+    const uint32_t probe = prefix | (1u << bit);
+    const float pf = __uint_as_float(probe);
+    int below = 0;
+#pragma unroll
+    for (int i = 0; i < kPerLane; ++i) below += (fabsf(v[i]) < pf) ? 1 : 0;
+    below += __shfl_xor(below, 32, 64);
+    if (idx >= below) prefix = probe;
+  }
+  return __uint_as_float(prefix);
+}
+
+// Smallest float >= d for a positive finite-or-infinite double d.
+__device__ __forceinline__ float round_up_f32(double d) {
+  float f = (float)d;
+  if ((double)f < d) f = __uint_as_float(__float_as_uint(f) + 1u);
+  return f;
+}
+
+struct QParams {
+  float zero;
+  float t1, t2, t3;       // thresholds on t = fl(x - zero), clip folded in
+  uint32_t meta;          // scale fp16 bits | zero fp16 bits << 16
+};
+
+__device__ QParams vector_params(const float (&v)[kPerLane], int clip_idx) {
+  float mx = v[0], mn = v[0];
+#pragma unroll
+  for (int i = 1; i < kPerLane; ++i) {
+    mx = fmaxf(mx, v[i]);
+    mn = fminf(mn, v[i]);
+  }
+  mx = fmaxf(mx, shfl_xor_f32(mx, 32));
+  mn = fminf(mn, shfl_xor_f32(mn, 32));
+  float thr = __builtin_inff();
+  if (clip_idx >= 0) {
+    thr = select_abs_rank(v, clip_idx);
+    mx = fminf(fmaxf(mx, -thr), thr);
+    mn = fminf(fmaxf(mn, -thr), thr);
+  }
+  float scale = (mx - mn) / 3.0f;                       // IEEE divide
+  scale = (scale > kScaleFloor) ? scale : kScaleFloor;
+  const uint16_t s16 = f32_to_f16_bits(scale);
+  const uint16_t z16 = f32_to_f16_bits(mn);
+  const float s = f16_bits_to_f32(s16);
+  const float z = f16_bits_to_f32(z16);
+  // q >= 1 <=> fl(t/s) >= 0.5 - 2^-25 <=> t/s >  0.5 - 3*2^-26
+  // q >= 2 <=> fl(t/s) >= 1.5        <=> t/s >= 1.5 - 2^-24
+  // q >= 3 <=> fl(t/s) >= 2.5        <=> t/s >= 2.5 - 2^-23
+  // s * c1 is never a float (odd 25-bit mantissa times s), so ">" and ">="
+  // both become t >= round_up(s * c1).
+  const double sd = (double)s;
+  float t1 = round_up_f32(sd * (0.5 - 3.0 * 0x1p-26));
+  float t2 = round_up_f32(sd * (1.5 - 0x1p-24));
+  float t3 = round_up_f32(sd * (2.5 - 0x1p-23));
+  if (clip_idx >= 0) {
+    // Clamping x to [-thr, thr] clamps t to [fl(-thr - z), fl(thr - z)]
+    // (x -> fl(x - z) is monotone), which moves a threshold to +-inf when it
+    // falls outside that range.
+    const float tlo = -thr - z;
+    const float thi = thr - z;
+    const float inf = __builtin_inff();
+    t1 = (t1 <= tlo) ? -inf : ((t1 > thi) ? inf : t1);
+    t2 = (t2 <= tlo) ? -inf : ((t2 > thi) ? inf : t2);
+    t3 = (t3 <= tlo) ? -inf : ((t3 > thi) ? inf : t3);
+  }
+  QParams p;
+  p.zero = z;
+  p.t1 = t1;
+  p.t2 = t2;
+  p.t3 = t3;
+  p.meta = (uint32_t)s16 | ((uint32_t)z16 << 16);
+  return p;
+}
+
+// Quantize, pack and store this lane's 128 codes (32 bytes) plus, on the
+// lower half lane, the 4 meta bytes of this side.
+__device__ void quantize_store(const float (&v)[kPerLane], const QParams& p, int64_t slot,
+                               int head, int side, int half, const CacheArgs& c) {
+  uint32_t words[8];
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    uint32_t acc = 0;
+#pragma unroll
+    for (int i = 15; i >= 0; --i) {
+      const float t = v[16 * w + i] - p.zero;
+      const bool a = t >= p.t2;
+      const bool b = t >= (a ? p.t3 : p.t1);
+      acc = (acc << 2) | ((a ? 2u : 0u) | (b ? 1u : 0u));
+    }
+    words[w] = acc;
+  }
+  if (slot < 0 || slot >= c.num_slots) return;
+  const int64_t page = slot / c.block_size;
+  const int64_t row = slot - page * c.block_size;
+  uint8_t* kslot = c.k_cache + page * c.k_page + row * c.k_tok + (int64_t)head * c.k_head;
+  uint8_t* dst;
+  if (side == 0) {
+    dst = kslot + kKCodeOff + 32 * half;
+  } else {
+    dst = c.v_cache + page * c.v_page + row * c.v_tok + (int64_t)head * c.v_head + 32 * half;
+  }
+  u32x4* d4 = reinterpret_cast<u32x4*>(dst);
+  d4[0] = u32x4{words[0], words[1], words[2], words[3]};
+  d4[1] = u32x4{words[4], words[5], words[6], words[7]};
+  if (half == 0) *reinterpret_cast<uint32_t*>(kslot + 4 * side) = p.meta;
+}
+
+// ---------------------------------------------------------------------------
+// Pre-rotated entry: fp32 rotated input [N, Hk, D] (token stride in elements).
+// grid = (ceil(N / 128), Hk * 2), block = 256 (4 waves x 32 tokens).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void quant_write_prerotated_kernel(
+    const float* __restrict__ k_rot, const float* __restrict__ v_rot, int64_t n_tokens,
+    int64_t token_stride, const int64_t* __restrict__ slots, CacheArgs c, int clip_k,
+    int clip_v) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int head = blockIdx.y >> 1;
+  const int side = blockIdx.y & 1;
+  const int half = lane >> 5;
+  const int64_t tok = (int64_t)blockIdx.x * 128 + wave * kTokPerWave + (lane & 31);
+  const bool live = tok < n_tokens;
+  const float* src = (side == 0 ? k_rot : v_rot) + (live ? tok : 0) * token_stride +
+                     (int64_t)head * kHeadDim + half * kPerLane;
+  float v[kPerLane];
+#pragma unroll
+  for (int i = 0; i < kPerLane; i += 4) {
+    floatx4 x = live ? *reinterpret_cast<const floatx4*>(src + i) : floatx4{0.f, 0.f, 0.f, 0.f};
+    v[i] = x[0];
+    v[i + 1] = x[1];
+    v[i + 2] = x[2];
+    v[i + 3] = x[3];
+  }
+  const QParams p = vector_params(v, side == 0 ? clip_k : clip_v);
+  quantize_store(v, p, live ? slots[tok] : -1, head, side, half, c);
+}
+
+// ---------------------------------------------------------------------------
+// Fused entry: bf16 input, rotation on MFMA.
+//
+// Rotation operand (prepared once per layer by oscar_rotation_operand):
+//   op[m][p][T][lane][u] (bf16), m = 16-row K step, p = 0 hi / 1 lo split,
+//   T = 32-feature output tile.  Entry = R[e][f] with
+//     e = 128*(lane >> 5) + 8*m + u                      (input feature)
+//     f = 128*((r >> 2) & 1) + 16*T + 4*(r >> 3) + (r & 3), r = lane & 31
+//   so that accumulator register i of tile T in lane l is feature
+//   128*(l >> 5) + 16*T + i of token (l & 31) — the per-lane layout above.
+// grid = (ceil(N / 256), Hk * 2), block = 512 (8 waves x 32 tokens); every
+// wave of a block shares the operand chunks streamed through LDS.
+// ---------------------------------------------------------------------------
+constexpr int kFusedWaves = 8;
+constexpr int kChunkBytes = 2 * 8 * 64 * 16;   // one K step: 2 passes x 8 tiles x 64 lanes x 16 B
+
+__global__ __launch_bounds__(512) void quant_write_fused_kernel(
+    const uint16_t* __restrict__ key, const uint16_t* __restrict__ value, int64_t n_tokens,
+    int64_t token_stride, const uint8_t* __restrict__ rot_k, const uint8_t* __restrict__ rot_v,
+    const int64_t* __restrict__ slots, CacheArgs c, int clip_k, int clip_v) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2][kChunkBytes];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int head = blockIdx.y >> 1;
+  const int side = blockIdx.y & 1;
+  const int half = lane >> 5;
+  const int64_t tok = (int64_t)blockIdx.x * (kFusedWaves * kTokPerWave) + wave * kTokPerWave + (lane & 31);
+  const bool live = tok < n_tokens;
+  const uint8_t* rop = side == 0 ? rot_k : rot_v;
+
+  // B operand: this lane's token, input features 128*half + 8m .. +7 for m = 0..15.
+  bf16x8 xb[16];
+  {
+    const uint16_t* src = (side == 0 ? key : value) + (live ? tok : 0) * token_stride +
+                          (int64_t)head * kHeadDim + half * kPerLane;
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      u32x4 raw = live ? *reinterpret_cast<const u32x4*>(src + 8 * m) : u32x4{0u, 0u, 0u, 0u};
+      xb[m] = __builtin_bit_cast(bf16x8, raw);
+    }
+  }
+
+  floatx16 acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc[t] = floatx16{};
+
+  // Stage K step 0.
+  const u32x4* gsrc = reinterpret_cast<const u32x4*>(rop);
+  constexpr int kVecPerChunk = kChunkBytes / 16;           // 1024 x 16 B
+  constexpr int kVecPerThread = kVecPerChunk / (kFusedWaves * 64);   // 2
+  u32x4 stage[kVecPerThread];
+#pragma unroll
+  for (int j = 0; j < kVecPerThread; ++j) stage[j] = gsrc[tid + j * kFusedWaves * 64];
+#pragma unroll
+  for (int j = 0; j < kVecPerThread; ++j)
+    reinterpret_cast<u32x4*>(lds[0])[tid + j * kFusedWaves * 64] = stage[j];
+  __syncthreads();
+
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const int buf = m & 1;
+    if (m + 1 < 16) {
+#pragma unroll
+      for (int j = 0; j < kVecPerThread; ++j)
+        stage[j] = gsrc[(m + 1) * kVecPerChunk + tid + j * kFusedWaves * 64];
+    }
+    const u32x4* a_src = reinterpret_cast<const u32x4*>(lds[buf]);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const bf16x8 a = __builtin_bit_cast(bf16x8, a_src[(p * 8 + t) * 64 + lane]);
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, xb[m], acc[t], 0, 0, 0);
+      }
+    }
+    if (m + 1 < 16) {
+#pragma unroll
+      for (int j = 0; j < kVecPerThread; ++j)
+        reinterpret_cast<u32x4*>(lds[buf ^ 1])[tid + j * kFusedWaves * 64] = stage[j];
+    }
+    __syncthreads();
+  }
+
+  float v[kPerLane];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[16 * t + i] = acc[t][i];
+  }
+  const QParams p = vector_params(v, side == 0 ? clip_k : clip_v);
+  quantize_store(v, p, live ? slots[tok] : -1, head, side, half, c);
+}
+
+// One thread per operand element (2 x 16 x 8 x 64 x 8 = 131072 entries).
+__global__ void rotation_operand_kernel(const float* __restrict__ R, __bf16* __restrict__ out) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= 2 * 16 * 8 * 64 * 8) return;
+  const int u = idx & 7;
+  const int lane = (idx >> 3) & 63;
+  const int t = (idx >> 9) & 7;
+  const int p = (idx >> 12) & 1;
+  const int m = idx >> 13;
+  const int r = lane & 31;
+  const int e = 128 * (lane >> 5) + 8 * m + u;
+  const int f = 128 * ((r >> 2) & 1) + 16 * t + 4 * (r >> 3) + (r & 3);
+  const float x = R[e * kHeadDim + f];
+  const __bf16 hi = (__bf16)x;
+  out[idx] = p == 0 ? hi : (__bf16)(x - (float)hi);
+}
+
+int check_cache_args(const CacheArgs& c) {
+  if (c.block_size <= 0 || c.num_slots <= 0 || c.k_cache == nullptr || c.v_cache == nullptr)
+    return kErrInvalidArgument;
+  if (c.k_head < kKCodeOff + kCodeBytes || c.v_head < kCodeBytes) return kErrUnsupportedGeometry;
+  const int64_t strides[6] = {c.k_page, c.k_tok, c.k_head, c.v_page, c.v_tok, c.v_head};
+  for (int64_t s : strides)
+    if (s <= 0 || (s & 15) != 0) return kErrUnsupportedGeometry;
+  if ((reinterpret_cast<uintptr_t>(c.k_cache) & 15) || (reinterpret_cast<uintptr_t>(c.v_cache) & 15))
+    return kErrUnsupportedGeometry;
+  return kOk;
+}
+
+}  // namespace
+}  // namespace oscar
+
+using namespace oscar;
+
+extern "C" {
+
+size_t oscar_rotation_operand_bytes(int32_t head_size) {
+  return head_size == kHeadDim ? (size_t)16 * kChunkBytes : 0;
+}
+
+int oscar_rotation_operand(const float* rotation, void* operand, int32_t head_size,
+                           hipStream_t stream) {
+  if (head_size != kHeadDim) return kErrUnsupportedHeadDim;
+  if (rotation == nullptr || operand == nullptr) return kErrInvalidArgument;
+  const int total = 2 * 16 * 8 * 64 * 8;
+  hipLaunchKernelGGL(rotation_operand_kernel, dim3((total + 255) / 256), dim3(256), 0, stream,
+                     rotation, static_cast<__bf16*>(operand));
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+int oscar_quant_write_prerotated(const float* k_rot, const float* v_rot, int64_t num_tokens,
+                                 int32_t num_kv_heads, int32_t head_size, int64_t token_stride,
+                                 const int64_t* slot_mapping, void* k_cache, void* v_cache,
+                                 int32_t block_size, int64_t num_pages, int64_t k_stride_page,
+                                 int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
+                                 int64_t v_stride_token, int64_t v_stride_head,
+                                 int32_t clip_index_k, int32_t clip_index_v, hipStream_t stream) {
+  if (head_size != kHeadDim) return kErrUnsupportedHeadDim;
+  if (num_tokens < 0 || num_kv_heads <= 0 || clip_index_k >= kHeadDim || clip_index_v >= kHeadDim)
+    return kErrInvalidArgument;
+  if (num_tokens == 0) return kOk;
+  if (k_rot == nullptr || v_rot == nullptr || slot_mapping == nullptr) return kErrInvalidArgument;
+  if (token_stride < (int64_t)num_kv_heads * kHeadDim || (token_stride & 3) ||
+      (reinterpret_cast<uintptr_t>(k_rot) & 15) || (reinterpret_cast<uintptr_t>(v_rot) & 15))
+    return kErrInvalidArgument;
+  CacheArgs c{static_cast<uint8_t*>(k_cache), static_cast<uint8_t*>(v_cache), k_stride_page,
+              k_stride_token, k_stride_head, v_stride_page, v_stride_token, v_stride_head,
+              block_size, num_pages * (int64_t)block_size};
+  int st = check_cache_args(c);
+  if (st != kOk) return st;
+  dim3 grid((unsigned)((num_tokens + 127) / 128), (unsigned)(num_kv_heads * 2));
+  hipLaunchKernelGGL(quant_write_prerotated_kernel, grid, dim3(256), 0, stream, k_rot, v_rot,
+                     num_tokens, token_stride, slot_mapping, c, (int)clip_index_k,
+                     (int)clip_index_v);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+int oscar_quant_write(const void* key_bf16, const void* value_bf16, int64_t num_tokens,
+                      int32_t num_kv_heads, int32_t head_size, int64_t token_stride,
+                      const void* rot_k_operand, const void* rot_v_operand,
+                      const int64_t* slot_mapping, void* k_cache, void* v_cache,
+                      int32_t block_size, int64_t num_pages, int64_t k_stride_page,
+                      int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
+                      int64_t v_stride_token, int64_t v_stride_head, int32_t clip_index_k,
+                      int32_t clip_index_v, hipStream_t stream) {
+  if (head_size != kHeadDim) return kErrUnsupportedHeadDim;
+  if (num_tokens < 0 || num_kv_heads <= 0 || clip_index_k >= kHeadDim || clip_index_v >= kHeadDim)
+    return kErrInvalidArgument;
+  if (num_tokens == 0) return kOk;
+  if (key_bf16 == nullptr || value_bf16 == nullptr || slot_mapping == nullptr ||
+      rot_k_operand == nullptr || rot_v_operand == nullptr)
+    return kErrInvalidArgument;
+  if (token_stride < (int64_t)num_kv_heads * kHeadDim || (token_stride & 7) ||
+      (reinterpret_cast<uintptr_t>(key_bf16) & 15) || (reinterpret_cast<uintptr_t>(value_bf16) & 15) ||
+      (reinterpret_cast<uintptr_t>(rot_k_operand) & 15) ||
+      (reinterpret_cast<uintptr_t>(rot_v_operand) & 15))
+    return kErrInvalidArgument;
+  CacheArgs c{static_cast<uint8_t*>(k_cache), static_cast<uint8_t*>(v_cache), k_stride_page,
+              k_stride_token, k_stride_head, v_stride_page, v_stride_token, v_stride_head,
+              block_size, num_pages * (int64_t)block_size};
+  int st = check_cache_args(c);
+  if (st != kOk) return st;
+  const int64_t per_block = kFusedWaves * kTokPerWave;
+  dim3 grid((unsigned)((num_tokens + per_block - 1) / per_block), (unsigned)(num_kv_heads * 2));
+  hipLaunchKernelGGL(quant_write_fused_kernel, grid, dim3(kFusedWaves * 64), 0, stream,
+                     static_cast<const uint16_t*>(key_bf16), static_cast<const uint16_t*>(value_bf16),
+                     num_tokens, token_stride, static_cast<const uint8_t*>(rot_k_operand),
+                     static_cast<const uint8_t*>(rot_v_operand), slot_mapping, c,
+                     (int)clip_index_k, (int)clip_index_v);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+}  // extern "C"

@@ -1,0 +1,153 @@
+"""GPU parity of kernel 1 (quantize-write) against the CPU oracle.
+
+* Pre-rotated entry: cache bytes bit-exact with the oracle store given the
+  same rotated fp32 input (whole caches compared, so pad bytes and bytes of
+  skipped slots must be untouched).
+* Fused entry (MFMA rotation): the rotation is computed in a different order
+  than the oracle's fp32 CPU matmul, so codes may differ only where a rotated
+  value sits within rounding distance of a bin edge.  Tolerances, stated:
+  >= 99.9 % of code bytes identical, every dequantized value within one
+  quantization step (max of the two scales) of the oracle's, meta scale within
+  2 fp16 ulps.
+"""
+import pytest
+import torch
+
+from oracle import format as ofmt
+from oracle import rotate as orot
+from oracle import store as ostore
+from oscar_amd import synthetic
+from oscar_amd.kernels import quant
+
+pytestmark = pytest.mark.gpu
+
+D = 256
+
+
+def make_caches(pages, bs, hk, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    width = D if dtype == torch.int8 else D
+    raw = torch.randint(0, 256, (2, pages, bs, hk, width * (1 if dtype == torch.int8 else 2)),
+                        generator=g, dtype=torch.uint8)
+    return [raw[i].view(dtype).clone() for i in range(2)]
+
+
+def oracle_store(k_rot, v_rot, caches, slots, ck, cv):
+    out = [c.clone() for c in caches]
+    N, hk, _ = k_rot.shape
+    kr = orot.clip(k_rot, ck)
+    vr = orot.clip(v_rot, cv)
+    ostore.store_ref(kr, vr, out[0], out[1], slots)
+    return out
+
+
+@pytest.mark.parametrize("cache_dtype", [torch.int8, torch.bfloat16])
+@pytest.mark.parametrize("hk", [1, 2])
+@pytest.mark.parametrize("ratios", [(0.96, 0.92), (0.0, 0.0), (0.5, 0.75), (1.0, 0.004)])
+def test_prerotated_bit_exact(device, cache_dtype, hk, ratios):
+    torch.manual_seed(0)
+    N, bs, pages = 300, 128, 6
+    k, v = synthetic.kv(N, hk, D, seed=11)
+    Rk, Rv = synthetic.rotations(D, seed=5)
+    k_rot = k.float() @ Rk
+    v_rot = v.float() @ Rv
+    perm = torch.randperm(pages * bs, generator=torch.Generator().manual_seed(3))[:N]
+    slots = perm.to(torch.int64)
+    slots[::7] = -1
+    caches = make_caches(pages, bs, hk, cache_dtype, seed=9)
+    expect = oracle_store(k_rot, v_rot, caches, slots, *ratios)
+    dev = [c.to(device) for c in caches]
+    quant.quant_write_prerotated(k_rot.to(device), v_rot.to(device), dev[0], dev[1], slots.to(device),
+                                 quant.clip_index(ratios[0], D), quant.clip_index(ratios[1], D))
+    torch.cuda.synchronize()
+    for got, want in zip(dev, expect):
+        diff = (got.cpu().view(torch.uint8) != want.view(torch.uint8)).sum().item()
+        assert diff == 0, f"{diff} bytes differ"
+
+
+def test_prerotated_edge_vectors(device):
+    """Constant vectors, ties at the clip threshold, exact bin edges, tiny ranges."""
+    hk, bs = 1, 16
+    rows = []
+    rows.append(torch.zeros(D))
+    rows.append(torch.full((D,), 1.0))
+    rows.append(torch.full((D,), -1.25))
+    rows.append(torch.full((D,), 1e-7))
+    x = torch.linspace(-3, 3, D)
+    rows.append(x)
+    rows.append(torch.round(x * 4) / 4)          # many ties
+    rows.append(torch.tensor([0.5, -0.5] * (D // 2)))
+    ramp = torch.arange(D, dtype=torch.float32) / 85.0   # values on exact bin edges
+    rows.append(ramp)
+    rows.append(1000.0 + torch.arange(D) * 1e-4)        # tiny range at large magnitude
+    rows.append(torch.where(torch.arange(D) % 2 == 0, 1.0, -1.0) * 65000.0)
+    k_rot = torch.stack(rows).unsqueeze(1).float()
+    v_rot = k_rot.flip(0).clone()
+    N = k_rot.shape[0]
+    slots = torch.arange(N, dtype=torch.int64)
+    for ratios in [(0.96, 0.92), (0.0, 0.0), (0.5, 0.5)]:
+        caches = [torch.zeros(2, bs, hk, D, dtype=torch.int8) for _ in range(2)]
+        expect = oracle_store(k_rot, v_rot, caches, slots, *ratios)
+        dev = [c.to(device) for c in caches]
+        quant.quant_write_prerotated(k_rot.to(device), v_rot.to(device), dev[0], dev[1], slots.to(device),
+                                     quant.clip_index(ratios[0], D), quant.clip_index(ratios[1], D))
+        torch.cuda.synchronize()
+        for got, want in zip(dev, expect):
+            assert torch.equal(got.cpu().view(torch.uint8), want.view(torch.uint8)), ratios
+
+
+def test_prerotated_large_random_write(device):
+    """65,536-token write with random slots and ~1/16 skipped (C5 write shape)."""
+    N, hk, bs = 65536, 1, 128
+    pages = N // bs + 8
+    g = torch.Generator().manual_seed(21)
+    k_rot = torch.randn(N, hk, D, generator=g) * 1.7
+    v_rot = torch.randn(N, hk, D, generator=g)
+    slots = torch.randperm(pages * bs, generator=g)[:N].to(torch.int64)
+    slots[torch.rand(N, generator=g) < 1 / 16] = -1
+    caches = [torch.zeros(pages, bs, hk, D, dtype=torch.int8) for _ in range(2)]
+    expect = oracle_store(k_rot, v_rot, caches, slots, 0.96, 0.92)
+    dev = [c.to(device) for c in caches]
+    quant.quant_write_prerotated(k_rot.to(device), v_rot.to(device), dev[0], dev[1], slots.to(device), 245, 235)
+    torch.cuda.synchronize()
+    for got, want in zip(dev, expect):
+        assert torch.equal(got.cpu().view(torch.uint8), want.view(torch.uint8))
+
+
+@pytest.mark.parametrize("hk", [1, 2])
+def test_fused_rotation_within_tolerance(device, hk):
+    N, bs, pages = 1000, 128, 9
+    k, v = synthetic.kv(N, hk, D, seed=13)
+    Rk, Rv = synthetic.rotations(D, seed=17)
+    slots = torch.randperm(pages * bs, generator=torch.Generator().manual_seed(2))[:N].to(torch.int64)
+    slots[::11] = -1
+    caches = [torch.zeros(pages, bs, hk, D, dtype=torch.int8) for _ in range(2)]
+    k_rot = orot.rotate_clip(k, Rk, 0.0)
+    v_rot = orot.rotate_clip(v, Rv, 0.0)
+    expect = oracle_store(k_rot, v_rot, caches, slots, 0.96, 0.92)
+    dev = [c.to(device) for c in caches]
+    ops = [quant.rotation_operand(R.to(device)) for R in (Rk, Rv)]
+    quant.quant_write(k.to(device), v.to(device), ops[0], ops[1], dev[0], dev[1], slots.to(device),
+                      245, 235, hk, D)
+    torch.cuda.synchronize()
+    valid = slots[slots >= 0]
+    got = ostore.logical_slots(dev[0].cpu(), dev[1].cpu(), valid, hk, D)
+    want = ostore.logical_slots(expect[0], expect[1], valid, hk, D)
+    codes = torch.cat([got[..., 32:96], got[..., 96:160]], -1)
+    codes_w = torch.cat([want[..., 32:96], want[..., 96:160]], -1)
+    same = (codes == codes_w).float().mean().item()
+    assert same >= 0.999, f"only {same:.5f} of code bytes match"
+    kg, vg = ofmt.parse_slot_bytes(got, D)
+    kw, vw = ofmt.parse_slot_bytes(want, D)
+    meta_g = [ofmt.f16_from_le(got[..., 2 * j:2 * j + 1], got[..., 2 * j + 1:2 * j + 2]) for j in range(4)]
+    meta_w = [ofmt.f16_from_le(want[..., 2 * j:2 * j + 1], want[..., 2 * j + 1:2 * j + 2]) for j in range(4)]
+    for (a, b), (sa, sb) in (((kg, kw), (meta_g[0], meta_w[0])), ((vg, vw), (meta_g[2], meta_w[2]))):
+        step = torch.maximum(sa, sb)
+        assert ((a - b).abs() <= step * 1.0001 + 1e-6).all()
+        assert ((sa - sb).abs() <= 2 * 2.0 ** -10 * sb.abs()).all()
+    # Untouched pages stay zero: nothing written outside the valid slots.
+    for c in dev:
+        flat = c.cpu().view(torch.uint8).reshape(pages * bs, -1)
+        mask = torch.ones(pages * bs, dtype=torch.bool)
+        mask[valid] = False
+        assert not flat[mask].any()
