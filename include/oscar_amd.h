@@ -81,6 +81,40 @@ int oscar_quant_write_prerotated(const float* k_rot, const float* v_rot, int64_t
                                  int64_t v_stride_token, int64_t v_stride_head,
                                  int32_t clip_index_k, int32_t clip_index_v, oscar_stream_t stream);
 
+/* ---------------------------------------------------------------- paged MTP decode
+ * Causal multi-token attention of short requests (<= 16 query tokens each)
+ * over their INT2 history plus the FP32 staging window, rotated domain.
+ * Replaces oscar_paged_attention_triton / _oscar_paged_stage1 +
+ * _oscar_decode_stage2 (oscar_ascend/kernels/paged_attention.py:272-360,
+ * decode_kernel.py:250-293) with the semantics of oscar_paged_attention_ref
+ * (paged_attention.py:41-64).
+ *   q_rot [num_tokens][Hq][D], k_new / v_new [num_tokens][Hk][D]: fp32 rotated;
+ *   block_table [num_requests][block_table_stride] int32 (block_table_cols used);
+ *   query_start_loc [num_requests + 1], seq_lens [num_requests] int32 (device);
+ *     request i owns query rows [qsl[i], qsl[i+1]) and history positions
+ *     0 .. seq_lens[i] - n_i - 1;
+ *   max_query_len / max_history: host upper bounds used to size the grid;
+ *   stage_k / stage_v [stage_rows][block_size][Hk][D] fp32 and stage_owner
+ *     [stage_rows][block_size] int64 (stage_rows = 0: no window);
+ *   out [num_tokens][Hq][D] fp32 (rotated-V domain);
+ *   workspace: >= oscar_paged_decode_workspace_bytes(...) bytes.
+ */
+size_t oscar_paged_decode_workspace_bytes(int32_t num_requests, int32_t num_kv_heads,
+                                          int32_t num_heads, int32_t max_query_len,
+                                          int64_t max_history);
+int oscar_paged_decode(const float* q_rot, const float* k_new, const float* v_new,
+                       int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                       int32_t head_size, const void* k_cache, const void* v_cache,
+                       int32_t block_size, int64_t num_pages, int64_t k_stride_page,
+                       int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
+                       int64_t v_stride_token, int64_t v_stride_head, const int32_t* block_table,
+                       int64_t block_table_stride, int32_t block_table_cols,
+                       const int32_t* query_start_loc, const int32_t* seq_lens,
+                       int32_t num_requests, int32_t max_query_len, int64_t max_history,
+                       const float* stage_k, const float* stage_v, const int64_t* stage_owner,
+                       int32_t stage_rows, float scale, float* out, void* workspace,
+                       size_t workspace_size, oscar_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,85 @@
+"""Host wrapper of the paged MTP decode kernel (kernel 2).
+
+Mirrors the reference seam ``oscar_paged_attention_triton(q, k, v, kc, vc, bt,
+qsl, seqs, scale, stage=None)`` (oscar_ascend/kernels/paged_attention.py:272-360):
+same arguments and meaning, rotated-domain fp32 inputs, rotated-V-domain fp32
+output [n, Hq, D].  ``qsl``/``seqs`` are host lists (the reference's
+metadata_batch_lists); they are validated exactly like the reference's
+query_layout (paged_attention.py:20-38) and uploaded once per call.
+"""
+from __future__ import annotations
+
+import itertools
+
+import torch
+
+from ..format import check_d
+from . import _lib
+from .quant import cache_geometry
+
+MAX_QUERY_LEN = 16          # rows per request <= 16 tokens x group (backend.py:277)
+
+_workspaces: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-device scratch for split partials, grown on demand (stream-ordered reuse)."""
+    key = (device.type, device.index)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def validate_layout(qsl, seqs):
+    """paged_attention.py:20-38 — lengths must be >= 0 and <= their sequence."""
+    lengths = [b - a for a, b in itertools.pairwise(qsl)]
+    if len(seqs) != len(lengths) or any(n < 0 or s < n for n, s in zip(lengths, seqs)):
+        raise ValueError("Invalid OSCAR query/sequence lengths")
+    return lengths
+
+
+def paged_attention(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None) -> torch.Tensor:
+    n, hq, d = q.shape
+    if n == 0:
+        return torch.empty_like(q, dtype=torch.float32)
+    check_d(d)
+    hk = k.shape[1]
+    lengths = validate_layout(qsl, seqs)
+    if sum(lengths) != n:
+        raise ValueError("Query layout does not match actual query tokens")
+    max_q = max(lengths) if lengths else 0
+    if max_q > MAX_QUERY_LEN:
+        raise ValueError(f"paged decode supports at most {MAX_QUERY_LEN} query tokens per request")
+    max_hist = max((s - m for s, m in zip(seqs, lengths)), default=0)
+    dev = q.device
+    q = q.float().contiguous()
+    k = k.float().contiguous()
+    v = v.float().contiguous()
+    bt = bt.to(device=dev, dtype=torch.int32).contiguous()
+    meta = torch.tensor(list(qsl) + list(seqs), dtype=torch.int32).to(dev, non_blocking=True)
+    qstart, seq_t = meta[:len(qsl)], meta[len(qsl):]
+    bs, pages, kst, vst = cache_geometry(kc, vc)
+    if stage is not None:
+        sk, sv, owner = stage
+        if sk.shape[1] != bs:
+            raise ValueError("staging arena block size must equal the cache block size")
+        sk, sv = sk.float().contiguous(), sv.float().contiguous()
+        owner = owner.to(torch.int64).contiguous()
+        rows = owner.shape[0]
+    else:
+        sk = sv = owner = None
+        rows = 0
+    B = len(lengths)
+    L = _lib.load()
+    need = L.oscar_paged_decode_workspace_bytes(B, hk, hq, max(max_q, 1), max_hist)
+    ws = workspace(dev, need)
+    out = torch.empty(n, hq, d, dtype=torch.float32, device=dev)
+    _lib.call("oscar_paged_decode", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), n, hq, hk, d,
+              _lib.ptr(kc), _lib.ptr(vc), bs, pages, *kst, *vst, _lib.ptr(bt),
+              bt.stride(0) if bt.ndim == 2 else 0, bt.shape[-1] if bt.numel() else 0,
+              _lib.ptr(qstart), _lib.ptr(seq_t), B, max_q, max_hist,
+              _lib.ptr(sk), _lib.ptr(sv), _lib.ptr(owner), rows, float(scale), _lib.ptr(out),
+              _lib.ptr(ws), ws.numel(), _lib.stream_handle(dev))
+    return out

@@ -1,0 +1,90 @@
+"""GPU parity of kernel 2 (paged MTP decode) against the CPU oracle.
+
+Oracle: oracle.attention.paged_attention_ref (restating
+oscar_ascend/kernels/paged_attention.py:41-64) on the same INT2 caches,
+staging arena and rotated q/k/v.  Tolerance (fp32 output, stated):
+max |gpu - oracle| <= 1e-3 * max |oracle|  (relative to the output scale).
+"""
+import pytest
+import torch
+
+from oracle import attention as oatt
+from oscar_amd.kernels import decode
+from tests.scenarios import decode_case
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-3
+
+
+def run_case(case, device, with_stage=True):
+    L = case.layer
+    q, k, v = case.rotated()
+    stage = L.stage() if with_stage else None
+    want = oatt.paged_attention_ref(q, k, v, L.k_cache, L.v_cache, case.bt, case.qsl, case.seqs,
+                                    L.scale, stage)
+    dstage = None if stage is None else tuple(t.to(device) for t in stage)
+    got = decode.paged_attention(q.to(device), k.to(device), v.to(device), L.k_cache.to(device),
+                                 L.v_cache.to(device), case.bt.to(device), case.qsl, case.seqs,
+                                 L.scale, dstage)
+    torch.cuda.synchronize()
+    got = got.cpu()
+    err = (got - want).abs().max().item()
+    scale = want.abs().max().item()
+    assert torch.isfinite(got).all()
+    assert err <= REL_TOL * max(scale, 1e-6), f"max err {err:.3e} vs output scale {scale:.3e}"
+    return got, want
+
+
+def test_c1_single_query_identity_pages(device):
+    case = decode_case([1024], [1], identity_pages=True, seed=1)
+    run_case(case, device)
+    run_case(case, device, with_stage=False)
+
+
+def test_mixed_requests_small_pages_and_window(device):
+    case = decode_case([5, 4, 0, 300, 129], [2, 3, 1, 4, 16], bs=16, seed=2, sink=16, recent=32,
+                       staging=64)
+    run_case(case, device)
+
+
+def test_empty_request_and_long_mtp(device):
+    # A request with no query tokens (qsl repeats) must be skipped.
+    case = decode_case([700, 40], [16, 4], seed=3)
+    L = case.layer
+    q, k, v = case.rotated()
+    qsl = [0, 0] + [x for x in case.qsl[1:]]
+    seqs = [7] + case.seqs
+    bt = torch.cat([case.bt[:1], case.bt])
+    want = oatt.paged_attention_ref(q, k, v, L.k_cache, L.v_cache, bt, qsl, seqs, L.scale, L.stage())
+    got = decode.paged_attention(q.to(device), k.to(device), v.to(device), L.k_cache.to(device),
+                                 L.v_cache.to(device), bt.to(device), qsl, seqs, L.scale,
+                                 tuple(t.to(device) for t in L.stage()))
+    torch.cuda.synchronize()
+    assert (got.cpu() - want).abs().max().item() <= REL_TOL * want.abs().max().item()
+
+
+@pytest.mark.parametrize("cache_dtype", [torch.int8, torch.bfloat16])
+def test_c2_mtp_24k_shuffled_pages(device, cache_dtype):
+    case = decode_case([24579], [4], seed=93, cache_dtype=cache_dtype)
+    run_case(case, device)
+
+
+def test_concurrent_requests_shared_pool(device):
+    g = torch.Generator().manual_seed(5)
+    hist = torch.randint(2048, 6000, (8,), generator=g).tolist()
+    case = decode_case(hist, [4] * 8, seed=6, pool_pages=512)
+    run_case(case, device)
+
+
+def test_window_disabled_matches_pure_int2(device):
+    case = decode_case([3000], [4], seed=8, window=False)
+    run_case(case, device, with_stage=False)
+
+
+def test_invalid_layout_rejected(device):
+    case = decode_case([10], [2], seed=9)
+    q, k, v = case.rotated()
+    with pytest.raises(ValueError):
+        decode.paged_attention(q.to(device), k.to(device), v.to(device), case.layer.k_cache.to(device),
+                               case.layer.v_cache.to(device), case.bt.to(device), [0, 2], [1], 0.0625)
