@@ -115,6 +115,49 @@ int oscar_paged_decode(const float* q_rot, const float* k_new, const float* v_ne
                        int32_t stage_rows, float scale, float* out, void* workspace,
                        size_t workspace_size, oscar_stream_t stream);
 
+/* ---------------------------------------------------------------- prefill continuation
+ * Causal attention of one request's num_new new tokens over its cached_len
+ * INT2 history tokens plus themselves (new token j sees keys 0 .. cached_len
+ * + j), f16 MFMA on dequantized tiles, fp32 softmax.  Replaces the dense
+ * read path of oscar_ascend/backend.py:361-415 (oscar_full_dequant +
+ * _stage_splice + oscar_prefill, kernels/dequant_kernel.py:105-116,
+ * kernels/prefill.py:69-72) for one request.
+ *   q_rot [num_new][Hq][D], k_new / v_new [num_new][Hk][D]: fp32 rotated;
+ *   block_table_row [block_table_cols] int32: the request's pages;
+ *   staging as in oscar_paged_decode; out [num_new][Hq][D] fp32 rotated-V.
+ */
+int oscar_prefill_continuation(const float* q_rot, const float* k_new, const float* v_new,
+                               int32_t num_new, int32_t num_heads, int32_t num_kv_heads,
+                               int32_t head_size, const void* k_cache, const void* v_cache,
+                               int32_t block_size, int64_t num_pages, int64_t k_stride_page,
+                               int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
+                               int64_t v_stride_token, int64_t v_stride_head,
+                               const int32_t* block_table_row, int32_t block_table_cols,
+                               int64_t cached_len, const float* stage_k, const float* stage_v,
+                               const int64_t* stage_owner, int32_t stage_rows, float scale,
+                               float* out, oscar_stream_t stream);
+
+/* ---------------------------------------------------------------- window write
+ * Record the step's tokens in the FP32 sink/recent staging arena.
+ * Replaces the torch body of _staging_write (oscar_ascend/backend.py:439-481)
+ * without host synchronisation.  Token t (< num_tokens, slot >= 0) of request
+ * i (query_start_loc[i] <= t < query_start_loc[i+1]) sits at absolute
+ * position seq_lens[i] - query_start_loc[i+1] + t and is kept when that is
+ * >= seq_lens[i] - recent or < sink_eff.  Per seat ((slot / block_size) %
+ * stage_rows, slot % block_size) the highest token index wins: owner = page
+ * (kept) or -1, and a kept winner stores key @ rot_k / value @ rot_v (fp32,
+ * unclipped).  key/value: bf16 [num_tokens][token_stride]; rot_*: fp32 [D][D];
+ * seat_winner: int32 [stage_rows][block_size] scratch that must hold -1 on
+ * entry and is left at -1.
+ */
+int oscar_staging_write(const void* key_bf16, const void* value_bf16, int64_t token_stride,
+                        const int64_t* slot_mapping, int32_t num_tokens,
+                        const int32_t* query_start_loc, const int32_t* seq_lens,
+                        int32_t num_requests, int32_t num_kv_heads, int32_t head_size,
+                        int32_t block_size, int32_t stage_rows, int32_t sink_eff, int32_t recent,
+                        const float* rot_k, const float* rot_v, float* stage_k, float* stage_v,
+                        int64_t* stage_owner, int32_t* seat_winner, oscar_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

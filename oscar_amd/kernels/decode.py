@@ -40,10 +40,25 @@ def validate_layout(qsl, seqs):
     return lengths
 
 
-def paged_attention(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None) -> torch.Tensor:
+class DecodePlan:
+    """Device-resident arguments of one decode launch; ``launch`` only enqueues.
+
+    Keeps every tensor it points at alive.  Launching a plan repeatedly (or
+    capturing it in a HIP graph) re-runs the same decode on the current stream.
+    """
+
+    def __init__(self, args: tuple, out: torch.Tensor, keep: list):
+        self.args = args
+        self.out = out
+        self.keep = keep
+
+    def launch(self) -> torch.Tensor:
+        _lib.call("oscar_paged_decode", *self.args, _lib.stream_handle(self.out.device))
+        return self.out
+
+
+def plan(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None, out=None) -> DecodePlan:
     n, hq, d = q.shape
-    if n == 0:
-        return torch.empty_like(q, dtype=torch.float32)
     check_d(d)
     hk = k.shape[1]
     lengths = validate_layout(qsl, seqs)
@@ -57,6 +72,8 @@ def paged_attention(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None) ->
     q = q.float().contiguous()
     k = k.float().contiguous()
     v = v.float().contiguous()
+    if bt.ndim != 2:
+        raise ValueError("block table must be [requests, pages]")
     bt = bt.to(device=dev, dtype=torch.int32).contiguous()
     meta = torch.tensor(list(qsl) + list(seqs), dtype=torch.int32).to(dev, non_blocking=True)
     qstart, seq_t = meta[:len(qsl)], meta[len(qsl):]
@@ -72,14 +89,19 @@ def paged_attention(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None) ->
         sk = sv = owner = None
         rows = 0
     B = len(lengths)
-    L = _lib.load()
-    need = L.oscar_paged_decode_workspace_bytes(B, hk, hq, max(max_q, 1), max_hist)
+    need = _lib.load().oscar_paged_decode_workspace_bytes(B, hk, hq, max(max_q, 1), max_hist)
     ws = workspace(dev, need)
-    out = torch.empty(n, hq, d, dtype=torch.float32, device=dev)
-    _lib.call("oscar_paged_decode", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), n, hq, hk, d,
-              _lib.ptr(kc), _lib.ptr(vc), bs, pages, *kst, *vst, _lib.ptr(bt),
-              bt.stride(0) if bt.ndim == 2 else 0, bt.shape[-1] if bt.numel() else 0,
-              _lib.ptr(qstart), _lib.ptr(seq_t), B, max_q, max_hist,
-              _lib.ptr(sk), _lib.ptr(sv), _lib.ptr(owner), rows, float(scale), _lib.ptr(out),
-              _lib.ptr(ws), ws.numel(), _lib.stream_handle(dev))
-    return out
+    if out is None:
+        out = torch.empty(n, hq, d, dtype=torch.float32, device=dev)
+    args = (_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), n, hq, hk, d, _lib.ptr(kc), _lib.ptr(vc), bs,
+            pages, *kst, *vst, _lib.ptr(bt), bt.stride(0), bt.shape[1], _lib.ptr(qstart),
+            _lib.ptr(seq_t), B, max_q, max_hist, _lib.ptr(sk), _lib.ptr(sv), _lib.ptr(owner), rows,
+            float(scale), _lib.ptr(out), _lib.ptr(ws), ws.numel())
+    return DecodePlan(args, out, [q, k, v, kc, vc, bt, meta, sk, sv, owner, ws])
+
+
+def paged_attention(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None) -> torch.Tensor:
+    """Rotated-domain paged MTP attention; returns fp32 [n, Hq, D]."""
+    if q.shape[0] == 0:
+        return torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    return plan(q, k, v, kc, vc, bt, qsl, seqs, scale, stage).launch()

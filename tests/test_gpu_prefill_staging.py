@@ -1,0 +1,105 @@
+"""GPU parity of the window write kernel and kernel 3 (prefill continuation).
+
+* Window write: owner tags bit-exact with the oracle arena
+  (restating oscar_ascend/backend.py:439-481); staged fp32 values within
+  1e-5 relative of the oracle's fp32 CPU rotation (summation order differs).
+* Prefill continuation: against the oracle dense path (history dequant +
+  window splice + causal SDPA, restating backend.py:361-415 and
+  kernels/decode_kernel.py:70-117) evaluated in fp32, as the reference's own
+  gate does (delivery/probe_prefill.py:266-281).  The kernel rounds its MFMA
+  operands to bf16; stated tolerance: the bf16 contract's max-abs 2e-2 plus
+  half a bf16 ulp of the oracle value, |gpu - oracle| <= 2e-2 + 2^-8 |oracle|.
+"""
+from types import SimpleNamespace as NS
+
+import pytest
+import torch
+
+from oracle import attention as oatt
+from oracle import store as ostore
+from oracle.staging import Arena
+from oscar_amd import synthetic
+from oscar_amd.kernels import prefill, staging
+from tests.scenarios import decode_case, metadata
+
+pytestmark = pytest.mark.gpu
+D = 256
+
+
+def _gpu_arena(arena, device):
+    sk = torch.zeros_like(arena.stage_k, device=device)
+    sv = torch.zeros_like(sk)
+    owner = torch.full(arena.owner.shape, -1, dtype=torch.int64, device=device)
+    winner = torch.full(arena.owner.shape, -1, dtype=torch.int32, device=device)
+    return sk, sv, owner, winner
+
+
+def _write_both(arena, gpu, key, value, md, Rk, Rv, device):
+    arena.write(key, value, md, Rk, Rv)
+    qsl, seqs = md.query_start_loc.tolist(), md.seq_lens.tolist()
+    B = len(seqs)
+    meta = torch.tensor(qsl + seqs, dtype=torch.int32, device=device)
+    sk, sv, owner, winner = gpu
+    staging.staging_write(key.to(device), value.to(device), md.slot_mapping.to(device), meta[:B + 1],
+                          meta[B + 1:], B, key.shape[1], D, arena.bs, arena.sink_eff, arena.recent,
+                          Rk.to(device), Rv.to(device), sk, sv, owner, winner)
+
+
+@pytest.mark.parametrize("bs,sink,recent,staging_tokens", [(4, 4, 4, 8), (16, 16, 32, 64), (128, 128, 256, 8192)])
+def test_window_write_matches_oracle_over_steps(device, bs, sink, recent, staging_tokens):
+    hk = 1
+    Rk, Rv = synthetic.rotations(D, seed=31)
+    arena = Arena.create(bs, hk, D, sink, recent, staging_tokens)
+    gpu = _gpu_arena(arena, device)
+    g = torch.Generator().manual_seed(7)
+    # Step 1: two requests prefill (hash collisions between pages), step 2: MTP
+    # writes with a padding request and a skipped slot, step 3: recycled pages.
+    pages = max(arena.rows * 3, 16)
+    steps = []
+    h0, h1 = 5 * bs + 3, 2 * bs + 1
+    perm = torch.randperm(pages, generator=g).to(torch.int32)
+    bt = torch.stack([perm[:8], perm[8:16]])
+    s0 = synthetic.slots_for(bt[0], 0, h0, bs)
+    s1 = synthetic.slots_for(bt[1], 0, h1, bs)
+    steps.append((torch.cat([s0, s1]), [0, h0, h0 + h1], [h0, h1]))
+    s2 = torch.cat([synthetic.slots_for(bt[0], h0, 4, bs), synthetic.slots_for(bt[1], h1, 4, bs)])
+    s2[5] = -1
+    steps.append((s2, [0, 4, 8, 8], [h0 + 4, h1 + 4, 1]))
+    s3 = synthetic.slots_for(bt[0].flip(0), 0, 3 * bs, bs)
+    steps.append((s3, [0, 3 * bs], [10 * bs]))
+    for i, (slots, qsl, seqs) in enumerate(steps):
+        k, v = synthetic.kv(slots.numel(), hk, D, seed=40 + i)
+        md = metadata(slots, qsl, seqs, bt)
+        _write_both(arena, gpu, k, v, md, Rk, Rv, device)
+        torch.cuda.synchronize()
+        sk, sv, owner, winner = (t.cpu() for t in gpu)
+        assert torch.equal(owner, arena.owner), f"owner tags differ at step {i}"
+        assert (winner == -1).all()
+        live = arena.owner >= 0
+        for got, want in ((sk, arena.stage_k), (sv, arena.stage_v)):
+            err = (got[live] - want[live]).abs().max().item() if live.any() else 0.0
+            assert err <= 1e-5 * max(1.0, want[live].abs().max().item()), err
+
+
+@pytest.mark.parametrize("window", [False, True])
+@pytest.mark.parametrize("hist,new", [(0, 40), (1500, 300), (3000, 700)])
+def test_prefill_continuation_matches_dense_oracle(device, window, hist, new):
+    case = decode_case([hist], [new], seed=hist + new, window=window, sink=128, recent=256)
+    L = case.layer
+    q, k, v = case.rotated()
+    stage = L.stage()
+    if hist > 0:
+        kc, vc = ostore.full_dequant_ref(L.k_cache, L.v_cache, case.bt[0], hist, 1, D)
+        if stage is not None:
+            kc, vc = L.arena.splice(case.bt[0], hist, kc, vc)
+    else:
+        kc = vc = torch.zeros(0, 1, D)
+    want = oatt.prefill_ref(q, k, v, kc, vc, L.scale, 1, D)
+    dstage = None if stage is None else tuple(t.to(device) for t in stage)
+    got = prefill.prefill_continuation(q.to(device), k.to(device), v.to(device), L.k_cache.to(device),
+                                       L.v_cache.to(device), case.bt[0].to(device), hist, L.scale, dstage)
+    torch.cuda.synchronize()
+    got = got.cpu()
+    err = (got - want).abs().max().item()
+    assert torch.isfinite(got).all()
+    assert ((got - want).abs() <= 2e-2 + 2.0 ** -8 * want.abs()).all(), f"max abs err {err:.3e}"
