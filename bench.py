@@ -39,61 +39,134 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def c2_case(seed=93):
-    from tests.scenarios import decode_case
+class LayerState:
+    """One FULL layer's state right before its decode read, written on the GPU
+    by the product write path (fused quantize-write + window-write kernels)."""
 
-    return decode_case([C2_HISTORY], [C2_QLEN], hq=HQ, hk=HK, bs=BS, seed=seed)
+    def __init__(self, impl, layer, caches, bt, qsl, seqs, q_rot, k_rot, v_rot):
+        self.impl, self.layer, self.caches, self.bt = impl, layer, caches, bt
+        self.qsl, self.seqs = qsl, seqs
+        self.q_rot, self.k_rot, self.v_rot = q_rot, k_rot, v_rot
+
+    def stage(self):
+        return self.impl._stage(self.layer)
 
 
-def decode_bytes(case) -> dict:
-    """Algorithmic HBM bytes of one C2 layer decode."""
-    L = case.layer
-    owner = L.arena.owner if L.arena is not None else None
-    hist = case.seqs[0] - C2_QLEN
-    staged = 0
-    if owner is not None:
-        pos = list(range(hist))
-        pages = case.bt[0][[p // BS for p in pos]].long()
-        rows = pages % owner.shape[0]
-        staged = int((owner[rows, [p % BS for p in pos]] == pages).sum())
-    int2 = (hist - staged) * HK * 136
-    window = staged * HK * 2 * D * 4
+def make_impl(dev):
+    from oscar_amd.backend import OscarAttentionBackendImpl
+
+    impl = OscarAttentionBackendImpl.__new__(OscarAttentionBackendImpl)
+    impl.head_size, impl.num_kv_heads, impl.num_heads = D, HK, HQ
+    impl.scale = D ** -0.5
+    impl.key_cache = impl.value_cache = None
+    import contextlib
+    import io
+
+    with contextlib.redirect_stdout(io.StringIO()):
+        impl._oscar_setup()
+    cfg = impl._oscar
+    cfg.k_clip_ratio, cfg.v_clip_ratio = 0.96, 0.92
+    cfg.sink_tokens, cfg.recent_tokens, cfg.staging_tokens = 128, 256, 8192
+    cfg.window_enabled = True
+    return impl
+
+
+def build_layer(dev, history: list, q_len: int, pool: int, seed: int) -> LayerState:
+    """Prefill-write every request's history, then write the MTP step's tokens."""
+    from types import SimpleNamespace as NS
+
+    import torch
+
+    from oscar_amd import synthetic
+
+    impl = make_impl(dev)
+    Rk, Rv = synthetic.rotations(D, seed)
+    layer = NS(layer_name="model.layers.0.self_attn.attn", _oscar_rots=(Rk.to(dev), Rv.to(dev)))
+    caches = [torch.zeros(pool, BS, HK, D, dtype=torch.int8, device=dev) for _ in range(2)]
+    B = len(history)
+    need = [(h + q_len + BS - 1) // BS for h in history]
+    perm = synthetic.page_permutation(pool, seed + 1)
+    T = max(need)
+    bt = torch.zeros(B, T, dtype=torch.int32)
+    off = 0
+    for i, n in enumerate(need):
+        bt[i, :n] = perm[off:off + n]
+        off += n
+
+    def write(counts, starts, seqs, kseed):
+        n = sum(counts)
+        k, v = synthetic.kv(n, HK, D, seed=kseed)
+        slots = torch.cat([synthetic.slots_for(bt[i], st, c, BS) for i, (st, c) in enumerate(zip(starts, counts))])
+        qsl = [0]
+        for c in counts:
+            qsl.append(qsl[-1] + c)
+        md = NS(num_actual_tokens=n, slot_mapping=slots.to(dev), query_start_loc_cpu=torch.tensor(qsl),
+                seq_lens_list=list(seqs), block_tables=bt.to(dev))
+        kd, vd = k.to(dev), v.to(dev)
+        impl.do_kv_cache_update(layer, kd, vd, caches, md.slot_mapping)
+        impl._ensure_staging(layer, caches)
+        impl._staging_write(layer, kd, vd, md)
+        return kd, vd, qsl
+
+    write(history, [0] * B, history, seed + 2)
+    seqs = [h + q_len for h in history]
+    kd, vd, qsl = write([q_len] * B, history, seqs, seed + 3)
+    q = synthetic.queries(q_len * B, HQ, D, seed=seed + 4).to(dev)
+    rk, rv = layer._oscar_rots
+    torch.cuda.synchronize()
+    return LayerState(impl, layer, caches, bt.to(dev), qsl, seqs, q.float() @ rk, kd.float() @ rk,
+                      vd.float() @ rv)
+
+
+def clone_layer(st: LayerState) -> LayerState:
+    from types import SimpleNamespace as NS
+
+    layer = NS(**vars(st.layer))
+    for name in ("_oscar_stage_k", "_oscar_stage_v", "_oscar_slot_owner", "_oscar_seat_winner"):
+        setattr(layer, name, getattr(st.layer, name).clone())
+    return LayerState(st.impl, layer, [c.clone() for c in st.caches], st.bt, st.qsl, st.seqs,
+                      st.q_rot, st.k_rot, st.v_rot)
+
+
+def decode_bytes(st: LayerState) -> dict:
+    """Algorithmic HBM bytes of one layer decode (counted per request)."""
+    import torch
+
+    owner = st.stage()[2].cpu() if st.stage() is not None else None
+    bt = st.bt.cpu()
+    n_q = st.q_rot.shape[0]
+    int2 = window = staged = 0
+    for i, (a, b) in enumerate(zip(st.qsl, st.qsl[1:])):
+        hist = st.seqs[i] - (b - a)
+        pos = torch.arange(hist)
+        pages = bt[i][pos // BS].long()
+        s_i = 0
+        if owner is not None:
+            s_i = int((owner[pages % owner.shape[0], pos % BS] == pages).sum())
+        staged += s_i
+        int2 += (hist - s_i) * HK * 136
+        window += s_i * HK * 2 * D * 4
     owner_tbl = owner.numel() * 8 if owner is not None else 0
-    qkv = C2_QLEN * HQ * D * 4 + C2_QLEN * HK * 2 * D * 4
-    out = C2_QLEN * HQ * D * 4
-    bt = case.bt.numel() * 4
-    total = int2 + window + owner_tbl + qkv + out + bt
-    return {"total": total, "int2": int2, "window": window, "staged_tokens": staged,
-            "int2_160B_variant": (hist - staged) * HK * 160 + window + owner_tbl + qkv + out + bt}
+    qkv = n_q * HQ * D * 4 + n_q * HK * 2 * D * 4
+    out = n_q * HQ * D * 4
+    bt_bytes = sum((s + BS - 1) // BS for s in st.seqs) * 4
+    fixed = window + owner_tbl + qkv + out + bt_bytes
+    hist_tokens = int2 // (HK * 136)
+    return {"total": int2 + fixed, "int2": int2, "window": window, "staged_tokens": staged,
+            "int2_160B_variant": hist_tokens * HK * 160 + fixed}
 
 
-def bench_decode(args, dev):
+def bench_decode(args, dev, history, q_len, pool, layers, seed=93):
     import torch
 
     from oscar_amd.kernels import decode
 
-    case = c2_case()
-    L = case.layer
-    q, k, v = case.rotated()
-    nbytes = decode_bytes(case)
-    plans = []
-    stage = L.stage()
-    for _ in range(args.layers):
-        kc, vc = L.k_cache.to(dev), L.v_cache.to(dev)
-        st = tuple(t.to(dev) for t in stage)
-        plans.append(decode.plan(q.to(dev), k.to(dev), v.to(dev), kc, vc, case.bt.to(dev),
-                                 case.qsl, case.seqs, L.scale, st))
+    base = build_layer(dev, history, q_len, pool, seed)
+    nbytes = decode_bytes(base)
+    states = [base] + [clone_layer(base) for _ in range(layers - 1)]
+    plans = [decode.plan(st.q_rot, st.k_rot, st.v_rot, st.caches[0], st.caches[1], st.bt, st.qsl,
+                         st.seqs, st.impl.scale, st.stage()) for st in states]
     torch.cuda.synchronize()
-    # Correctness gate on layer 0 before timing.
-    from oracle import attention as oatt
-
-    want = oatt.paged_attention_ref(q, k, v, L.k_cache, L.v_cache, case.bt, case.qsl, case.seqs,
-                                    L.scale, stage)
-    got = plans[0].launch().cpu()
-    err = (got - want).abs().max().item() / want.abs().max().item()
-    if not err <= 1e-3:
-        raise SystemExit(f"decode parity gate failed: rel err {err:.3e}")
-
     side = torch.cuda.Stream(dev)
     side.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(side):
@@ -105,8 +178,8 @@ def bench_decode(args, dev):
     with torch.cuda.graph(graph):
         for p in plans:
             p.launch()
-    reps_w = max(1, args.warmup // args.layers)
-    reps = max(1, args.steps // args.layers)
+    reps_w = max(1, args.warmup // layers)
+    reps = max(1, args.steps // layers)
     for _ in range(reps_w):
         graph.replay()
     torch.cuda.synchronize()
@@ -117,12 +190,13 @@ def bench_decode(args, dev):
         graph.replay()
     e1.record(stream)
     e1.synchronize()
-    steps = reps * args.layers
+    steps = reps * layers
     ms = e0.elapsed_time(e1)
-    us_per_layer = ms * 1000.0 / steps
-    gbps = nbytes["total"] / (us_per_layer * 1e-6) / 1e9
-    return {"us_per_layer": us_per_layer, "steps": steps, "ms": ms, "gbps": gbps, "bytes": nbytes,
-            "parity_rel_err": err, "case": case}
+    us = ms * 1000.0 / steps
+    out0 = plans[0].launch().clone()
+    torch.cuda.synchronize()
+    return {"us_per_layer": us, "steps": steps, "ms": ms, "gbps": nbytes["total"] / (us * 1e-6) / 1e9,
+            "bytes": nbytes, "state": base, "out0": out0, "warmup": reps_w * layers}
 
 
 def bench_quant_write(args, dev):
@@ -171,21 +245,28 @@ def bench_quant_write(args, dev):
             "valid_slots": valid}
 
 
-def cpu_baseline(case, seconds: float):
+def cpu_baseline(st, gpu_out, seconds: float):
+    """The oracle's read path on the same (GPU-written) C2 state, on this host.
+
+    Also the parity gate of the measured kernel: its output must match the
+    oracle within the fp32 contract (1e-3 relative to the output scale).
+    """
     import torch
 
     from oracle import attention as oatt
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    L = case.layer
-    q, k, v = case.rotated()
-    stage = L.stage()
+    q, k, v = st.q_rot.cpu(), st.k_rot.cpu(), st.v_rot.cpu()
+    kc, vc = st.caches[0].cpu(), st.caches[1].cpu()
+    bt = st.bt.cpu()
+    stage = tuple(t.cpu() for t in st.stage()) if st.stage() is not None else None
 
     def once():
-        oatt.paged_attention_ref(q, k, v, L.k_cache, L.v_cache, case.bt, case.qsl, case.seqs, L.scale, stage)
+        return oatt.paged_attention_ref(q, k, v, kc, vc, bt, st.qsl, st.seqs, st.impl.scale, stage)
 
-    once()
+    want = once()
+    rel = (gpu_out.cpu() - want).abs().max().item() / max(want.abs().max().item(), 1e-30)
     samples = []
     t_end = time.perf_counter() + seconds
     while time.perf_counter() < t_end or len(samples) < 6:
@@ -197,10 +278,11 @@ def cpu_baseline(case, seconds: float):
         model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
     except Exception:
         model = "unknown"
-    return {"value": med * 1e6, "unit": "us/layer", "cores": cores, "kind": "port",
-            "sample": f"median of {len(samples)} runs of the oracle C2 read path "
-                      f"(dequant 24579-token INT2 history + FP32 window splice + causal SDPA, "
-                      f"4 queries x 6 heads); host CPU {model}"}
+    base = {"value": round(med * 1e6, 1), "unit": "us/layer", "cores": cores, "kind": "port",
+            "sample": f"median of {len(samples)} runs (~{seconds:.0f} s) of the oracle read path on the C2 "
+                      f"layer state (dequant 24579-token INT2 history + FP32 window splice + causal SDPA, "
+                      f"4 queries x 6 heads, fp32); host CPU {model}"}
+    return base, rel
 
 
 def main():
@@ -223,21 +305,23 @@ def main():
         raise SystemExit("bench.py needs a GPU")
     dev = torch.device("cuda:0")
     log("bench: decode C2")
-    dec = bench_decode(args, dev)
+    dec = bench_decode(args, dev, [C2_HISTORY], C2_QLEN, pool=193, layers=args.layers)
     log(f"bench: decode {dec['us_per_layer']:.3f} us/layer; quant-write C5")
     qw = bench_quant_write(args, dev)
     log(f"bench: quant-write {qw['gbps']:.1f} GB/s")
-    cpu = None
+    cpu, rel = None, None
     if not args.no_cpu_baseline:
-        log("bench: cpu baseline")
-        cpu = cpu_baseline(dec["case"], args.cpu_seconds)
+        log("bench: cpu baseline + parity gate")
+        cpu, rel = cpu_baseline(dec["state"], dec["out0"], args.cpu_seconds)
+        if not rel <= 1e-3:
+            raise SystemExit(f"decode parity gate failed: rel err {rel:.3e}")
     line = {
         "metric": METRIC,
         "value": round(dec["us_per_layer"], 4),
         "unit": "us/layer",
         "n_gpus": 1,
         "steps": dec["steps"],
-        "warmup": max(1, args.warmup // args.layers) * args.layers,
+        "warmup": dec["warmup"],
         "ms_per_step": dec["us_per_layer"] / 1000.0,
         "higher_is_better": False,
         "scaling": "weak",
@@ -253,7 +337,7 @@ def main():
             "decode_bytes_per_layer": dec["bytes"]["total"],
             "decode_bytes_per_layer_160B_variant": dec["bytes"]["int2_160B_variant"],
             "staged_tokens": dec["bytes"]["staged_tokens"],
-            "decode_parity_rel_err": dec["parity_rel_err"],
+            "decode_parity_rel_err_vs_oracle": rel,
             "quant_write": {"workload": "C5 write: 65536 tokens bf16, Hk=1, random slots ~1/16 skipped, "
                                         "rotation on MFMA, clip 0.96/0.92",
                             "us_per_call": round(qw["us_per_call"], 3), "gbps": round(qw["gbps"], 1),
