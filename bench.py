@@ -52,7 +52,7 @@ class LayerState:
         return self.impl._stage(self.layer)
 
 
-def make_impl(dev):
+def make_impl(dev, window=True):
     from oscar_amd.backend import OscarAttentionBackendImpl
 
     impl = OscarAttentionBackendImpl.__new__(OscarAttentionBackendImpl)
@@ -67,11 +67,11 @@ def make_impl(dev):
     cfg = impl._oscar
     cfg.k_clip_ratio, cfg.v_clip_ratio = 0.96, 0.92
     cfg.sink_tokens, cfg.recent_tokens, cfg.staging_tokens = 128, 256, 8192
-    cfg.window_enabled = True
+    cfg.window_enabled = window
     return impl
 
 
-def build_layer(dev, history: list, q_len: int, pool: int, seed: int) -> LayerState:
+def build_layer(dev, history: list, q_len: int, pool: int, seed: int, window=True) -> LayerState:
     """Prefill-write every request's history, then write the MTP step's tokens."""
     from types import SimpleNamespace as NS
 
@@ -79,7 +79,7 @@ def build_layer(dev, history: list, q_len: int, pool: int, seed: int) -> LayerSt
 
     from oscar_amd import synthetic
 
-    impl = make_impl(dev)
+    impl = make_impl(dev, window)
     Rk, Rv = synthetic.rotations(D, seed)
     layer = NS(layer_name="model.layers.0.self_attn.attn", _oscar_rots=(Rk.to(dev), Rv.to(dev)))
     caches = [torch.zeros(pool, BS, HK, D, dtype=torch.int8, device=dev) for _ in range(2)]
@@ -104,8 +104,9 @@ def build_layer(dev, history: list, q_len: int, pool: int, seed: int) -> LayerSt
                 seq_lens_list=list(seqs), block_tables=bt.to(dev))
         kd, vd = k.to(dev), v.to(dev)
         impl.do_kv_cache_update(layer, kd, vd, caches, md.slot_mapping)
-        impl._ensure_staging(layer, caches)
-        impl._staging_write(layer, kd, vd, md)
+        if window:
+            impl._ensure_staging(layer, caches)
+            impl._staging_write(layer, kd, vd, md)
         return kd, vd, qsl
 
     write(history, [0] * B, history, seed + 2)
@@ -123,7 +124,8 @@ def clone_layer(st: LayerState) -> LayerState:
 
     layer = NS(**vars(st.layer))
     for name in ("_oscar_stage_k", "_oscar_stage_v", "_oscar_slot_owner", "_oscar_seat_winner"):
-        setattr(layer, name, getattr(st.layer, name).clone())
+        if hasattr(st.layer, name):
+            setattr(layer, name, getattr(st.layer, name).clone())
     return LayerState(st.impl, layer, [c.clone() for c in st.caches], st.bt, st.qsl, st.seqs,
                       st.q_rot, st.k_rot, st.v_rot)
 
@@ -161,11 +163,11 @@ def bench_decode(args, dev, history, q_len, pool, layers, seed=93):
 
     from oscar_amd.kernels import decode
 
-    base = build_layer(dev, history, q_len, pool, seed)
+    base = build_layer(dev, history, q_len, pool, seed, window=bool(args.window))
     nbytes = decode_bytes(base)
     states = [base] + [clone_layer(base) for _ in range(layers - 1)]
     plans = [decode.plan(st.q_rot, st.k_rot, st.v_rot, st.caches[0], st.caches[1], st.bt, st.qsl,
-                         st.seqs, st.impl.scale, st.stage()) for st in states]
+                         st.seqs, st.impl.scale, st.stage(), tiles_per_split=args.tps) for st in states]
     torch.cuda.synchronize()
     side = torch.cuda.Stream(dev)
     side.wait_stream(torch.cuda.current_stream(dev))
@@ -294,6 +296,9 @@ def main():
     ap.add_argument("--qw-iters", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--tps", type=int, default=0, help="decode tiles per split (0: automatic)")
+    ap.add_argument("--skip-quant-write", action="store_true")
+    ap.add_argument("--window", type=int, default=1, help="diagnostic: 0 disables the FP32 window")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (one TP rank's share "
@@ -306,9 +311,11 @@ def main():
     dev = torch.device("cuda:0")
     log("bench: decode C2")
     dec = bench_decode(args, dev, [C2_HISTORY], C2_QLEN, pool=193, layers=args.layers)
-    log(f"bench: decode {dec['us_per_layer']:.3f} us/layer; quant-write C5")
-    qw = bench_quant_write(args, dev)
-    log(f"bench: quant-write {qw['gbps']:.1f} GB/s")
+    log(f"bench: decode {dec['us_per_layer']:.3f} us/layer ({dec['gbps']:.1f} GB/s)")
+    qw = None
+    if not args.skip_quant_write:
+        qw = bench_quant_write(args, dev)
+        log(f"bench: quant-write {qw['gbps']:.1f} GB/s")
     cpu, rel = None, None
     if not args.no_cpu_baseline:
         log("bench: cpu baseline + parity gate")
@@ -338,7 +345,7 @@ def main():
             "decode_bytes_per_layer_160B_variant": dec["bytes"]["int2_160B_variant"],
             "staged_tokens": dec["bytes"]["staged_tokens"],
             "decode_parity_rel_err_vs_oracle": rel,
-            "quant_write": {"workload": "C5 write: 65536 tokens bf16, Hk=1, random slots ~1/16 skipped, "
+            "quant_write": None if qw is None else {"workload": "C5 write: 65536 tokens bf16, Hk=1, random slots ~1/16 skipped, "
                                         "rotation on MFMA, clip 0.96/0.92",
                             "us_per_call": round(qw["us_per_call"], 3), "gbps": round(qw["gbps"], 1),
                             "frac_of_hbm_peak": round(qw["gbps"] / HBM_PEAK_GBPS, 4),

@@ -96,12 +96,14 @@ int oscar_quant_write_prerotated(const float* k_rot, const float* v_rot, int64_t
  *   max_query_len / max_history: host upper bounds used to size the grid;
  *   stage_k / stage_v [stage_rows][block_size][Hk][D] fp32 and stage_owner
  *     [stage_rows][block_size] int64 (stage_rows = 0: no window);
+ *   tiles_per_split: 32-token tiles per split workgroup (0: automatic);
  *   out [num_tokens][Hq][D] fp32 (rotated-V domain);
- *   workspace: >= oscar_paged_decode_workspace_bytes(...) bytes.
+ *   workspace: >= oscar_paged_decode_workspace_bytes(...) bytes (same
+ *     tiles_per_split).  block_size must be a multiple of 32.
  */
 size_t oscar_paged_decode_workspace_bytes(int32_t num_requests, int32_t num_kv_heads,
                                           int32_t num_heads, int32_t max_query_len,
-                                          int64_t max_history);
+                                          int64_t max_history, int32_t tiles_per_split);
 int oscar_paged_decode(const float* q_rot, const float* k_new, const float* v_new,
                        int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
                        int32_t head_size, const void* k_cache, const void* v_cache,
@@ -112,8 +114,8 @@ int oscar_paged_decode(const float* q_rot, const float* k_new, const float* v_ne
                        const int32_t* query_start_loc, const int32_t* seq_lens,
                        int32_t num_requests, int32_t max_query_len, int64_t max_history,
                        const float* stage_k, const float* stage_v, const int64_t* stage_owner,
-                       int32_t stage_rows, float scale, float* out, void* workspace,
-                       size_t workspace_size, oscar_stream_t stream);
+                       int32_t stage_rows, float scale, int32_t tiles_per_split, float* out,
+                       void* workspace, size_t workspace_size, oscar_stream_t stream);
 
 /* ---------------------------------------------------------------- prefill continuation
  * Causal attention of one request's num_new new tokens over its cached_len

@@ -29,11 +29,12 @@ SIGNATURES = {
     "oscar_quant_write_prerotated": (_c_i32, [_c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i64, _c_p,
                                               _c_p, _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64,
                                               _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_p]),
-    "oscar_paged_decode_workspace_bytes": (_c_sz, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i64]),
+    "oscar_paged_decode_workspace_bytes": (_c_sz, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32]),
     "oscar_paged_decode": (_c_i32, [_c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_p,
                                     _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                     _c_p, _c_i64, _c_i32, _c_p, _c_p, _c_i32, _c_i32, _c_i64,
-                                    _c_p, _c_p, _c_p, _c_i32, _c_f32, _c_p, _c_p, _c_sz, _c_p]),
+                                    _c_p, _c_p, _c_p, _c_i32, _c_f32, _c_i32, _c_p, _c_p, _c_sz,
+                                    _c_p]),
     "oscar_prefill_continuation": (_c_i32, [_c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_p,
                                             _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                             _c_i64, _c_i64, _c_p, _c_i32, _c_i64, _c_p, _c_p, _c_p,

@@ -57,7 +57,8 @@ class DecodePlan:
         return self.out
 
 
-def plan(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None, out=None) -> DecodePlan:
+def plan(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None, out=None,
+         tiles_per_split: int = 0) -> DecodePlan:
     n, hq, d = q.shape
     check_d(d)
     hk = k.shape[1]
@@ -89,14 +90,16 @@ def plan(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None, out=None) -> 
         sk = sv = owner = None
         rows = 0
     B = len(lengths)
-    need = _lib.load().oscar_paged_decode_workspace_bytes(B, hk, hq, max(max_q, 1), max_hist)
+    if bs % 32:
+        raise ValueError("paged decode needs a cache block size that is a multiple of 32")
+    need = _lib.load().oscar_paged_decode_workspace_bytes(B, hk, hq, max(max_q, 1), max_hist, tiles_per_split)
     ws = workspace(dev, need)
     if out is None:
         out = torch.empty(n, hq, d, dtype=torch.float32, device=dev)
     args = (_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), n, hq, hk, d, _lib.ptr(kc), _lib.ptr(vc), bs,
             pages, *kst, *vst, _lib.ptr(bt), bt.stride(0), bt.shape[1], _lib.ptr(qstart),
             _lib.ptr(seq_t), B, max_q, max_hist, _lib.ptr(sk), _lib.ptr(sv), _lib.ptr(owner), rows,
-            float(scale), _lib.ptr(out), _lib.ptr(ws), ws.numel())
+            float(scale), int(tiles_per_split), _lib.ptr(out), _lib.ptr(ws), ws.numel())
     return DecodePlan(args, out, [q, k, v, kc, vc, bt, meta, sk, sv, owner, ws])
 
 

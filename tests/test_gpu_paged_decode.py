@@ -43,7 +43,7 @@ def test_c1_single_query_identity_pages(device):
 
 
 def test_mixed_requests_small_pages_and_window(device):
-    case = decode_case([5, 4, 0, 300, 129], [2, 3, 1, 4, 16], bs=16, seed=2, sink=16, recent=32,
+    case = decode_case([5, 4, 0, 300, 129], [2, 3, 1, 4, 16], bs=32, seed=2, sink=32, recent=32,
                        staging=64)
     run_case(case, device)
 
