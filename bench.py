@@ -1,6 +1,6 @@
 """Benchmark of the OSCAR INT2 KV-cache hot path on one MI355X.
 
-Headline (BASELINE metric): 4-token MTP decode attention over a 24,579-token
+Headline metric: 4-token MTP decode attention over a 24,579-token
 INT2 history (Hq=6, Hk=1, D=256, 193 shuffled 128-token pages, FP32
 sink/recent window) in microseconds per layer and achieved HBM GB/s, plus the
 quantize-write GB/s of a 65,536-token bulk write (random slots, ~1/16

@@ -2,7 +2,7 @@
 
 gcc -O2 -ffp-contract=off (no fast-math): every fp32 operation rounds once.
 The reference itself is Python (no compiled path), so there is no
-``oracle/_ref`` build; see DESIGN.md.
+``oracle/_ref`` build.
 """
 from __future__ import annotations
 

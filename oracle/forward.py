@@ -5,9 +5,12 @@ do_kv_cache_update / _prefill_attention (oscar_ascend/backend.py:150-189,
 239-319, 361-415).  Test infrastructure only; every tensor stays on the CPU.
 
 Routing mirrors the reference's paged route (backend.py:273-303): requests
-with 0 < q_len <= 16 use the fp32 paged MTP semantics; longer requests use the
-dense continuation semantics (history dequant + staged splice, attention in
-the query dtype).  Padding rows stay zero.
+with 0 < q_len <= paged_max_qlen (16) use the fp32 paged MTP semantics; longer
+requests use the dense continuation semantics (history dequant + staged
+splice, attention in the query dtype; backend.py:361-412).  paged_max_qlen = 0
+gives the reference's default dense route (OSCAR_ASCEND_USE_PAGED unset,
+backend.py:306-307), where every request takes the dense semantics.  Padding
+rows stay zero.
 """
 from __future__ import annotations
 
@@ -37,6 +40,7 @@ class OracleLayer:
     sink: int = 64
     recent: int = 256
     staging: int = 8192
+    paged_max_qlen: int = PAGED_MAX_QLEN
     arena: Arena | None = field(default=None)
 
     @property
@@ -85,7 +89,7 @@ class OracleLayer:
             if n <= 0:
                 continue
             bt_row = md.block_tables[i]
-            if n <= PAGED_MAX_QLEN:
+            if n <= self.paged_max_qlen:
                 res = attention.paged_attention_ref(
                     query[a:b].float() @ Rk, key[a:b].float() @ Rk, value[a:b].float() @ Rv,
                     self.k_cache, self.v_cache, bt_row.unsqueeze(0), [0, n], [seqs[i]],

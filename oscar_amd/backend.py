@@ -12,7 +12,7 @@ Write path (every step with fresh K/V):
                         unclipped fp32 rotated window values (kernels/staging.py)
 Read path, per request (backend.py:273-313 routing):
   0 < q_len <= 16    -> paged MTP decode kernel over INT2 history + window
-  q_len > 16         -> prefill-continuation kernel (bf16 MFMA over dequantized
+  q_len > 16         -> prefill-continuation kernel (f16 MFMA over dequantized
                         history tiles + the new tokens, right-aligned causal)
 Both read kernels work in the rotated domain; q/k/v are rotated with one
 fp32 matmul each and the output is mapped back with R_v^T.

@@ -43,13 +43,31 @@ def fixed_bytes_per_layer(head_dim: int, num_kv_heads: int, block_size: int, sin
     return fixed
 
 
+DECODE_TILE = 32                       # history tokens per decode tile
+DECODE_ROWS = 32                       # (query, head) rows per partial
+DECODE_PARTIAL_FLOATS = DECODE_ROWS * 256 + 2 * DECODE_ROWS
+
+
+def decode_tiles_per_split(max_requests: int, num_kv_heads: int, max_history: int) -> int:
+    """The library's default split length (in tiles) for this batch shape."""
+    tiles = -(-max_history // DECODE_TILE) if max_history > 0 else 0
+    work = tiles * max_requests * num_kv_heads
+    tps = 8
+    while tps < 64 and work // tps > 1024:
+        tps *= 2
+    return tps
+
+
 def decode_workspace_bytes(max_requests: int, num_kv_heads: int, num_heads: int, max_query_len: int,
-                           max_history: int) -> int:
-    """Same formula as oscar_paged_decode_workspace_bytes (no library needed)."""
-    group = num_heads // num_kv_heads
-    tiles = (max_query_len * group + 31) // 32
-    chunks = (max_history + 127) // 128
-    return max_requests * num_kv_heads * chunks * tiles * (256 * 32 + 64) * 4
+                           max_history: int, tiles_per_split: int = 0) -> int:
+    """Same value as oscar_paged_decode_workspace_bytes (no library needed):
+    one fp32 partial (32 rows x 256 + max + sum) per (request, kv head,
+    split, row tile)."""
+    tps = tiles_per_split or decode_tiles_per_split(max_requests, num_kv_heads, max_history)
+    tiles = -(-max_history // DECODE_TILE) if max_history > 0 else 0
+    splits = -(-tiles // tps)
+    row_tiles = -(-(max_query_len * (num_heads // num_kv_heads)) // DECODE_ROWS)
+    return max_requests * num_kv_heads * splits * row_tiles * DECODE_PARTIAL_FLOATS * 4
 
 
 def kv_block_bytes(block_size: int, num_kv_heads: int, slot_width: int, layers: int) -> int:

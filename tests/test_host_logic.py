@@ -1,0 +1,248 @@
+"""Host-side logic of the drop-in: configuration, rotation checkpoints,
+metadata accessors, plugin surgery and memory budgeting.  CPU only; the
+library is loaded (no GPU call is made).
+
+Restates the reference's host tests: tests/test_backend.py:108-115 (no device
+read of query starts), 135-149 (failed surgery restores class and state),
+218-223 (budget), 226-243 (layer verification), 246-252 (strict rotation),
+tests/test_numeric.py:172-182, 216-244, 274-296, 369-378, 441-486.
+"""
+import os
+from types import SimpleNamespace as NS
+
+import pytest
+import torch
+
+from oracle.staging import arena_geometry
+from oscar_amd import integration, plugin, rotation
+from oscar_amd.backend import OscarAttentionBackendImpl, metadata_batch_lists
+from oscar_amd.config import OscarConfig
+
+ENV_KEYS = [k for k in os.environ if k.startswith("OSCAR_ASCEND_")]
+
+
+@pytest.fixture
+def clean_env(monkeypatch):
+    for k in ENV_KEYS:
+        monkeypatch.delenv(k, raising=False)
+    return monkeypatch
+
+
+# ---------------------------------------------------------------- config
+def test_config_defaults(clean_env):
+    cfg = OscarConfig.from_env(256)
+    assert (cfg.sink_tokens, cfg.recent_tokens, cfg.staging_tokens) == (64, 256, 8192)
+    assert cfg.window_enabled and cfg.use_paged
+    assert (cfg.k_clip_ratio, cfg.v_clip_ratio) == (0.0, 0.0)
+    assert cfg.slot_bytes == 160 and cfg.data_bytes == 64 and cfg.levels == 4
+
+
+def test_config_env_keys(clean_env):
+    clean_env.setenv("OSCAR_ASCEND_K_CLIP_RATIO", "0.96")
+    clean_env.setenv("OSCAR_ASCEND_V_CLIP_RATIO", "0.92")
+    clean_env.setenv("OSCAR_ASCEND_SINK_TOKENS", "-5")
+    clean_env.setenv("OSCAR_ASCEND_RECENT_TOKENS", "0")
+    clean_env.setenv("OSCAR_ASCEND_STAGING_TOKENS", "bogus")
+    clean_env.setenv("OSCAR_ASCEND_USE_PAGED", "0")
+    cfg = OscarConfig.from_env(256)
+    assert (cfg.k_clip_ratio, cfg.v_clip_ratio) == (0.96, 0.92)
+    assert cfg.sink_tokens == 0 and cfg.staging_tokens == 8192
+    assert not cfg.window_enabled and not cfg.use_paged
+    clean_env.setenv("OSCAR_ASCEND_K_CLIP_RATIO", "1.5")
+    with pytest.raises(ValueError):
+        OscarConfig.from_env(256)
+    clean_env.setenv("OSCAR_ASCEND_K_CLIP_RATIO", "0.5")
+    clean_env.setenv("OSCAR_ASCEND_GROUP_SIZE", "64")
+    with pytest.raises(ValueError):
+        OscarConfig.from_env(256)
+
+
+# ---------------------------------------------------------------- rotations
+def test_layer_index_from_name():
+    assert rotation.layer_index_from_name("model.layers.11.self_attn.attn") == 11
+    assert rotation.layer_index_from_name("decoder.block7") == 7
+    assert rotation.layer_index_from_name("attn") is None
+
+
+def test_rotation_checkpoint_formats(tmp_path):
+    g = torch.Generator().manual_seed(0)
+    R1, R2, R3 = (torch.linalg.qr(torch.randn(64, 64, generator=g)).Q for _ in range(3))
+    name = "model.layers.11.self_attn.attn"
+    p = tmp_path / "layers.pt"
+    torch.save({"layers": {"model.layers.11.self_attn": {"rotation": R1, "rotation_v": R2},
+                           "3": {"rotation": R3}}}, p)
+    assert torch.equal(rotation.get_layer_rotation(str(p), name, 64, "cpu"), R1)
+    assert torch.equal(rotation.get_layer_rotation(str(p), name, 64, "cpu", mode="v"), R2)
+    assert torch.equal(rotation.get_layer_rotation(str(p), "model.layers.3.x", 64, "cpu", mode="v"), R3)
+    assert torch.equal(rotation.get_layer_rotation(str(p), "model.layers.4.x", 64, "cpu"), torch.eye(64))
+    p2 = tmp_path / "flat.pt"
+    torch.save({11: R2, "12": {"rotation": R3}}, p2)
+    assert torch.equal(rotation.get_layer_rotation(str(p2), name, 64, "cpu"), R2)
+    assert torch.equal(rotation.get_layer_rotation(str(p2), "model.layers.12.a", 64, "cpu"), R3)
+    p3 = tmp_path / "stacked.pt"
+    torch.save(torch.stack([R1, R2, R3]), p3)
+    assert torch.equal(rotation.get_layer_rotation(str(p3), "model.layers.2.a", 64, "cpu"), R3)
+    assert torch.equal(rotation.get_layer_rotation("", name, 64, "cpu"), torch.eye(64))
+
+
+def test_rotation_strict_mode(tmp_path):
+    p = tmp_path / "r.pt"
+    torch.save({"layers": {"1": {"rotation": torch.eye(64)}, "2": {"rotation": 2 * torch.eye(64)},
+                           "5": {"rotation": torch.eye(32)}}}, p)
+    with pytest.raises(ValueError, match="missing layer"):
+        rotation.get_layer_rotation(str(p), "model.layers.0.self_attn.attn", 64, "cpu", strict=True)
+    with pytest.raises(ValueError, match="orthogonal"):
+        rotation.get_layer_rotation(str(p), "model.layers.2.self_attn.attn", 64, "cpu", strict=True)
+    with pytest.raises(ValueError, match="shape"):
+        rotation.get_layer_rotation(str(p), "model.layers.5.self_attn.attn", 64, "cpu")
+
+
+def test_rotation_loader_refuses_pickled_objects(tmp_path):
+    p = tmp_path / "evil.pt"
+    torch.save({"layers": {"1": {"rotation": torch.eye(4), "obj": NS(x=1)}}}, p)
+    with pytest.raises(Exception):
+        rotation.get_layer_rotation(str(p), "model.layers.1.a", 4, "cpu")
+
+
+# ---------------------------------------------------------------- metadata
+def test_metadata_lists_do_not_read_device_query_starts():
+    class NoRead:
+        def tolist(self):
+            raise AssertionError("unexpected device sync")
+
+    md = NS(query_start_loc=NoRead(), actual_seq_lengths_q=[1, 2], seq_lens=NoRead(), seq_lens_list=[9, 12])
+    assert metadata_batch_lists(md) == ([0, 1, 2], [9, 12])
+
+
+def test_metadata_lists_multi_element_tensors_and_fallbacks():
+    m = NS(query_start_loc=torch.tensor([0, 16384, 16389]), query_start_loc_cpu=torch.tensor([0, 16384, 16389]),
+           seq_lens=torch.tensor([16384, 5]), seq_lens_cpu=torch.tensor([16384, 5]))
+    assert metadata_batch_lists(m) == ([0, 16384, 16389], [16384, 5])
+    m2 = NS(query_start_loc=torch.tensor([0, 3]), query_start_loc_cpu=None, seq_lens=torch.tensor([1000]),
+            seq_lens_cpu=None)
+    assert metadata_batch_lists(m2) == ([0, 3], [1000])
+    m3 = NS(query_start_loc=[0, 5], query_start_loc_cpu=None, seq_lens=[8], seq_lens_cpu=None)
+    assert metadata_batch_lists(m3) == ([0, 5], [8])
+    m4 = NS(query_start_loc=[0, 5], seq_lens=[8], _seq_lens_cpu=torch.tensor([7]))
+    assert metadata_batch_lists(m4) == ([0, 5], [7])
+
+
+# ---------------------------------------------------------------- plugin
+def test_failed_surgery_restores_class_and_state():
+    class Original:
+        pass
+
+    class Broken(Original):
+        def _oscar_setup(self):
+            self.partial = True
+            raise ValueError("unsupported")
+
+    impl = Original()
+    impl.keep = 123
+    with pytest.raises(ValueError):
+        plugin.install_impl(impl, Broken)
+    assert type(impl) is Original and vars(impl) == {"keep": 123}
+
+
+def test_surgery_installs_oscar_over_native_class(clean_env):
+    class NativeImpl:
+        def __init__(self):
+            self.head_size, self.num_heads, self.num_kv_heads = 256, 6, 1
+            self.scale = 0.0625
+
+        def forward(self, *a):
+            return "native"
+
+    impl = NativeImpl()
+    cls = plugin.oscar_class_for(NativeImpl)
+    assert plugin.oscar_class_for(NativeImpl) is cls and plugin.oscar_class_for(cls) is cls
+    plugin.install_impl(impl, cls)
+    assert isinstance(impl, OscarAttentionBackendImpl) and isinstance(impl, NativeImpl)
+    assert impl.forward.__func__ is OscarAttentionBackendImpl.forward
+    assert impl._oscar.head_dim == 256
+
+
+def test_surgery_rejects_other_head_sizes(clean_env):
+    class NativeImpl:
+        head_size, num_heads, num_kv_heads, scale = 128, 8, 1, 0.08
+
+    impl = NativeImpl()
+    with pytest.raises(ValueError, match="head_size"):
+        plugin.install_impl(impl, plugin.oscar_class_for(NativeImpl))
+    assert type(impl) is NativeImpl
+
+
+def test_hybrid_detection():
+    assert plugin._is_hybrid_config(NS(hf_text_config=NS(layer_types=["linear_attention", "attention"])))
+    assert not plugin._is_hybrid_config(NS(hf_text_config=NS(layer_types=["attention", "attention"])))
+    assert plugin._is_hybrid_config(NS(is_hybrid=True))
+
+
+def test_mtp_draft_layers_stay_native(capsys):
+    plugin._SKIP_REASONS_LOGGED.clear()
+    assert plugin._should_oscar(NS(layer_name="model.mtp.layers.0.self_attn.attn"), None) is False
+    assert plugin._should_oscar(NS(layer_name="mtp.block.attn"), None) is False
+    assert plugin._SKIP_REASONS_LOGGED == {"mtp-draft"}
+
+
+# ---------------------------------------------------------------- impl host checks
+def make_impl(clean_env):
+    impl = OscarAttentionBackendImpl.__new__(OscarAttentionBackendImpl)
+    impl.head_size, impl.num_kv_heads, impl.num_heads = 256, 1, 6
+    impl.scale = 0.0625
+    impl.key_cache = impl.value_cache = None
+    impl._oscar_setup()
+    return impl
+
+
+def test_cache_geometry_checks(clean_env):
+    impl = make_impl(clean_env)
+    impl._set_caches([torch.zeros(2, 128, 1, 256, dtype=torch.int8) for _ in range(2)])
+    impl._oscar_geo_ok = False
+    impl._set_caches([torch.zeros(2, 128, 1, 256, dtype=torch.bfloat16) for _ in range(2)])
+    impl._oscar_geo_ok = False
+    with pytest.raises(ValueError):
+        impl._set_caches([torch.zeros(2, 128, 1, 64, dtype=torch.int8) for _ in range(2)])
+    impl._oscar_geo_ok = False
+    with pytest.raises(ValueError):
+        impl._set_caches([torch.zeros(2, 1, 128, 256, dtype=torch.int8).transpose(1, 2) for _ in range(2)])
+
+
+def test_forward_without_metadata_zeroes_output(clean_env):
+    impl = make_impl(clean_env)
+    out = torch.full((3, 6, 256), 5.0)
+    caches = [torch.zeros(2, 128, 1, 256, dtype=torch.int8) for _ in range(2)]
+    assert torch.count_nonzero(impl.forward(NS(layer_name="l.0"), out, out, out, caches, None, output=out)) == 0
+
+
+# ---------------------------------------------------------------- budgeting
+def test_budget_accounts_shadow_and_fixed_buffers():
+    budget = integration.memory_budget(10000, 100, 25, 1000)
+    assert budget == 7200 and budget + (budget // 100) * 25 + 1000 <= 10000
+    with pytest.raises(ValueError):
+        integration.memory_budget(100, 100, 25, 100)
+
+
+def test_verify_layers():
+    integration.verify_layers(["linear_attention", "full_attention"], [1])
+    with pytest.raises(RuntimeError):
+        integration.verify_layers(["full_attention"] * 2, [0])
+    with pytest.raises(RuntimeError):
+        integration.verify_layers(["linear_attention"], [])
+
+
+@pytest.mark.parametrize("bs", [16, 32, 64, 128])
+def test_arena_rows_match_oracle_geometry(bs):
+    for sink in (0, 16, 64, 128, 200):
+        for recent in (0, 1, 128, 256, 300):
+            for staging in (0, 64, 8192):
+                assert integration.arena_rows(bs, sink, recent, staging) == arena_geometry(bs, sink, recent,
+                                                                                           staging)[3]
+
+
+def test_plan_capacity_fits_one_mi355x():
+    plan = integration.plan_capacity(integration.MI355X_HBM_BYTES - 20 * 10 ** 9, layers=16)
+    assert plan["blocks"] * plan["native_per_block"] + plan["fixed"] <= plan["available"]
+    assert plan["tokens"] == plan["blocks"] * 128
+    # one INT2 token of one layer costs 2 * 256 bytes of int8-geometry slots
+    assert plan["native_per_block"] == 2 * 128 * 256 * 16
