@@ -131,13 +131,16 @@ def clone_layer(st: LayerState) -> LayerState:
 
 
 def decode_bytes(st: LayerState) -> dict:
-    """Algorithmic HBM bytes of one layer decode (counted per request)."""
+    """Algorithmic HBM bytes of one layer decode: every history token's INT2
+    slot bytes (8 meta + 64 K + 64 V codes), the staged fp32 K/V of tokens the
+    window owns, the owner table, q / new k / new v / out in fp32 and the
+    block-table entries."""
     import torch
 
     owner = st.stage()[2].cpu() if st.stage() is not None else None
     bt = st.bt.cpu()
     n_q = st.q_rot.shape[0]
-    int2 = window = staged = 0
+    hist_tokens = window = staged = 0
     for i, (a, b) in enumerate(zip(st.qsl, st.qsl[1:])):
         hist = st.seqs[i] - (b - a)
         pos = torch.arange(hist)
@@ -146,14 +149,14 @@ def decode_bytes(st: LayerState) -> dict:
         if owner is not None:
             s_i = int((owner[pages % owner.shape[0], pos % BS] == pages).sum())
         staged += s_i
-        int2 += (hist - s_i) * HK * 136
+        hist_tokens += hist
         window += s_i * HK * 2 * D * 4
+    int2 = hist_tokens * HK * 136
     owner_tbl = owner.numel() * 8 if owner is not None else 0
     qkv = n_q * HQ * D * 4 + n_q * HK * 2 * D * 4
     out = n_q * HQ * D * 4
     bt_bytes = sum((s + BS - 1) // BS for s in st.seqs) * 4
     fixed = window + owner_tbl + qkv + out + bt_bytes
-    hist_tokens = int2 // (HK * 136)
     return {"total": int2 + fixed, "int2": int2, "window": window, "staged_tokens": staged,
             "int2_160B_variant": hist_tokens * HK * 160 + fixed}
 
@@ -247,6 +250,38 @@ def bench_quant_write(args, dev):
             "valid_slots": valid}
 
 
+def copy_probe(dev, mib: int) -> None:
+    """A plain device-to-device copy of known size (reads and writes `mib` MiB
+    per launch), the reference point for scaling PMC byte counters."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"bench: copy probe {mib} MiB x 4")
+
+
+def traffic_from_profile(kernel_src: Path):
+    """HBM bytes per decode call from the committed PMC summary, if it was
+    measured on the current kernel source (sha256 recorded in the summary)."""
+    import hashlib
+
+    prof = ROOT / "profiles" / "decode_c2_traffic.txt"
+    if not prof.exists():
+        return None
+    fields = dict(l.split(":", 1) for l in prof.read_text().splitlines() if ":" in l and not l.startswith(" "))
+    digest = hashlib.sha256(kernel_src.read_bytes()).hexdigest()
+    if fields.get("source_sha256", "").strip() != digest:
+        return None
+    try:
+        return int(fields["traffic_bytes_per_call"].strip())
+    except (KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(st, gpu_out, seconds: float):
     """The oracle's read path on the same (GPU-written) C2 state, on this host.
 
@@ -299,6 +334,8 @@ def main():
     ap.add_argument("--tps", type=int, default=0, help="decode tiles per split (0: automatic)")
     ap.add_argument("--skip-quant-write", action="store_true")
     ap.add_argument("--window", type=int, default=1, help="diagnostic: 0 disables the FP32 window")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="run a plain device copy of this many MiB first (PMC byte-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (one TP rank's share "
@@ -309,6 +346,8 @@ def main():
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
     dev = torch.device("cuda:0")
+    if args.copy_probe_mib > 0:
+        copy_probe(dev, args.copy_probe_mib)
     log("bench: decode C2")
     dec = bench_decode(args, dev, [C2_HISTORY], C2_QLEN, pool=193, layers=args.layers)
     log(f"bench: decode {dec['us_per_layer']:.3f} us/layer ({dec['gbps']:.1f} GB/s)")
@@ -352,7 +391,8 @@ def main():
                             "bytes_per_call": qw["bytes"]},
         },
         "roofline": {"bound": "hbm", "achieved": round(dec["gbps"], 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(dec["gbps"] / HBM_PEAK_GBPS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(dec["gbps"] / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic_from_profile(ROOT / "oscar_amd" / "csrc" / "paged_decode.hip")},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
