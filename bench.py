@@ -123,8 +123,9 @@ def clone_layer(st: LayerState) -> LayerState:
     from types import SimpleNamespace as NS
 
     layer = NS(**vars(st.layer))
-    for name in ("_oscar_stage_k", "_oscar_stage_v", "_oscar_slot_owner", "_oscar_seat_winner"):
-        if hasattr(st.layer, name):
+    for name in ("_oscar_stage_k", "_oscar_stage_v", "_oscar_slot_owner", "_oscar_seat_winner",
+                 "_oscar_stage_kimg", "_oscar_stage_vimg"):
+        if getattr(st.layer, name, None) is not None:
             setattr(layer, name, getattr(st.layer, name).clone())
     return LayerState(st.impl, layer, [c.clone() for c in st.caches], st.bt, st.qsl, st.seqs,
                       st.q_rot, st.k_rot, st.v_rot)
@@ -297,7 +298,7 @@ def cpu_baseline(st, gpu_out, seconds: float):
     q, k, v = st.q_rot.cpu(), st.k_rot.cpu(), st.v_rot.cpu()
     kc, vc = st.caches[0].cpu(), st.caches[1].cpu()
     bt = st.bt.cpu()
-    stage = tuple(t.cpu() for t in st.stage()) if st.stage() is not None else None
+    stage = tuple(t.cpu() for t in st.stage()[:3]) if st.stage() is not None else None
 
     def once():
         return oatt.paged_attention_ref(q, k, v, kc, vc, bt, st.qsl, st.seqs, st.impl.scale, stage)

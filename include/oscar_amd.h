@@ -90,16 +90,21 @@ int oscar_quant_write_prerotated(const float* k_rot, const float* v_rot, int64_t
  * (paged_attention.py:41-64).
  *   q_rot [num_tokens][Hq][D], k_new / v_new [num_tokens][Hk][D]: fp32 rotated;
  *   block_table [num_requests][block_table_stride] int32 (block_table_cols used);
- *   query_start_loc [num_requests + 1], seq_lens [num_requests] int32 (device);
- *     request i owns query rows [qsl[i], qsl[i+1]) and history positions
- *     0 .. seq_lens[i] - n_i - 1;
+ *   query_start_loc [num_requests + 1], seq_lens [num_requests] int32 in HOST
+ *     memory (the reference passes them as host lists; they are copied into
+ *     the kernel arguments, up to 128 requests per launch, larger batches are
+ *     launched in chunks); request i owns query rows [qsl[i], qsl[i+1]) and
+ *     history positions 0 .. seq_lens[i] - n_i - 1;
  *   max_query_len / max_history: host upper bounds used to size the grid;
- *   stage_k / stage_v [stage_rows][block_size][Hk][D] fp32 and stage_owner
- *     [stage_rows][block_size] int64 (stage_rows = 0: no window);
- *   tiles_per_split: 32-token tiles per split workgroup (0: automatic);
+ *   stage_owner [stage_rows][block_size] int64 and the window's fp16 operand
+ *     images stage_k_image / stage_v_image [stage_rows][block_size / 32][Hk]
+ *     [8192] (16-byte aligned, written by oscar_staging_write; stage_rows =
+ *     0: no window);
+ *   tiles_per_split: 32-token tiles per split workgroup (0: automatic, at most 256);
  *   out [num_tokens][Hq][D] fp32 (rotated-V domain);
  *   workspace: >= oscar_paged_decode_workspace_bytes(...) bytes (same
- *     tiles_per_split).  block_size must be a multiple of 32.
+ *     tiles_per_split); sized for one chunk of at most 128 requests.
+ *     block_size must be a multiple of 32.
  */
 size_t oscar_paged_decode_workspace_bytes(int32_t num_requests, int32_t num_kv_heads,
                                           int32_t num_heads, int32_t max_query_len,
@@ -113,9 +118,10 @@ int oscar_paged_decode(const float* q_rot, const float* k_new, const float* v_ne
                        int64_t block_table_stride, int32_t block_table_cols,
                        const int32_t* query_start_loc, const int32_t* seq_lens,
                        int32_t num_requests, int32_t max_query_len, int64_t max_history,
-                       const float* stage_k, const float* stage_v, const int64_t* stage_owner,
-                       int32_t stage_rows, float scale, int32_t tiles_per_split, float* out,
-                       void* workspace, size_t workspace_size, oscar_stream_t stream);
+                       const int64_t* stage_owner, const void* stage_k_image,
+                       const void* stage_v_image, int32_t stage_rows, float scale,
+                       int32_t tiles_per_split, float* out, void* workspace,
+                       size_t workspace_size, oscar_stream_t stream);
 
 /* ---------------------------------------------------------------- prefill continuation
  * Causal attention of one request's num_new new tokens over its cached_len
@@ -150,7 +156,10 @@ int oscar_prefill_continuation(const float* q_rot, const float* k_new, const flo
  * (kept) or -1, and a kept winner stores key @ rot_k / value @ rot_v (fp32,
  * unclipped).  key/value: bf16 [num_tokens][token_stride]; rot_*: fp32 [D][D];
  * seat_winner: int32 [stage_rows][block_size] scratch that must hold -1 on
- * entry and is left at -1.
+ * entry and is left at -1.  stage_k_image / stage_v_image (both or neither,
+ * block_size % 32 == 0): fp16 [stage_rows][block_size / 32][Hk][8192]; a
+ * kept winner also writes its values there in the decode kernel's MFMA
+ * operand order.
  */
 int oscar_staging_write(const void* key_bf16, const void* value_bf16, int64_t token_stride,
                         const int64_t* slot_mapping, int32_t num_tokens,
@@ -158,7 +167,8 @@ int oscar_staging_write(const void* key_bf16, const void* value_bf16, int64_t to
                         int32_t num_requests, int32_t num_kv_heads, int32_t head_size,
                         int32_t block_size, int32_t stage_rows, int32_t sink_eff, int32_t recent,
                         const float* rot_k, const float* rot_v, float* stage_k, float* stage_v,
-                        int64_t* stage_owner, int32_t* seat_winner, oscar_stream_t stream);
+                        int64_t* stage_owner, int32_t* seat_winner, void* stage_k_image,
+                        void* stage_v_image, oscar_stream_t stream);
 
 #ifdef __cplusplus
 }

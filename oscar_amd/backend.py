@@ -179,6 +179,12 @@ class OscarAttentionBackendImpl:
         layer._oscar_stage_v = torch.zeros_like(layer._oscar_stage_k)
         layer._oscar_slot_owner = torch.full((rows, bs), -1, dtype=torch.int64, device=dev)
         layer._oscar_seat_winner = torch.full((rows, bs), -1, dtype=torch.int32, device=dev)
+        # fp16 operand images of the window for the paged decode (32-token tiles)
+        layer._oscar_stage_kimg = layer._oscar_stage_vimg = None
+        if bs % 32 == 0:
+            shape = staging.image_shape(rows, bs, self.num_kv_heads)
+            layer._oscar_stage_kimg = torch.zeros(shape, dtype=torch.float16, device=dev)
+            layer._oscar_stage_vimg = torch.zeros(shape, dtype=torch.float16, device=dev)
         layer._oscar_stage_rows = rows
         layer._oscar_stage_ready = True
         self._oscar_stage_ready = True
@@ -207,11 +213,12 @@ class OscarAttentionBackendImpl:
         staging.staging_write(key, value, attn_metadata.slot_mapping[:N].to(dev), meta[:B + 1], meta[B + 1:],
                               B, self.num_kv_heads, self.head_size, bs, sink_eff, self._oscar.recent_tokens,
                               rk, rv, layer._oscar_stage_k, layer._oscar_stage_v, layer._oscar_slot_owner,
-                              layer._oscar_seat_winner)
+                              layer._oscar_seat_winner, layer._oscar_stage_kimg, layer._oscar_stage_vimg)
 
     def _stage(self, layer):
         if self._oscar.window_enabled and getattr(layer, "_oscar_stage_ready", False):
-            return layer._oscar_stage_k, layer._oscar_stage_v, layer._oscar_slot_owner
+            return (layer._oscar_stage_k, layer._oscar_stage_v, layer._oscar_slot_owner,
+                    layer._oscar_stage_kimg, layer._oscar_stage_vimg)
         return None
 
     # ------------------------------------------------------------------ forward

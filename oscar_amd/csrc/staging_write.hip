@@ -11,6 +11,16 @@
 // Kernel 1 records the winning token index per seat with atomicMax into a
 // persistent int32 array that starts (and is left) at -1.  Kernel 2: one block
 // per token; the winner updates owner / values and resets its seat to -1.
+//
+// A kept winner also refreshes the fp16 operand images the decode kernel
+// reads for window-owned tokens, per (arena row, 32-token tile, kv head):
+//   K image [16 k-steps m][64 lanes][8 slots]: lane t + 32g, slot 2i + b of
+//     step m = 2j + a holds feature 128g + 16j + 4a + i + 8b of token t;
+//   V image [2 h][4 sp][2 mm][64 lanes][8 slots]: lane c + 32gs holds feature
+//     4(32h + c) + sp; slot 4hi + {0, 2, 1, 3}[w] holds token 16mm + 8hi +
+//     4gs + w.
+// Both are exactly the MFMA operand registers of a wavefront, so the decode
+// copies them to LDS with 16-byte-per-lane direct loads.
 #include "oscar_common.h"
 
 namespace oscar {
@@ -35,7 +45,25 @@ struct StageArgs {
   float* stage_v;
   int64_t* owner;           // [rows][bs]
   int32_t* winner;          // [rows][bs], -1 between calls
+  _Float16* kimg;           // [rows][bs / 32][Hk][8192] or null
+  _Float16* vimg;
 };
+
+constexpr int kImgHalfs = 16 * 64 * 8;
+
+// Offsets of feature f of token t (0..31 within its tile) in the two images.
+__device__ __forceinline__ int kimg_offset(int f, int t) {
+  const int g = f >> 7, rr = f & 127, jj = rr >> 4, r16 = rr & 15, b = r16 >> 3, r8 = r16 & 7;
+  const int m = 2 * jj + (r8 >> 2), u = 2 * (r8 & 3) + b;
+  return (m * 64 + t + 32 * g) * 8 + u;
+}
+
+__device__ __forceinline__ int vimg_offset(int f, int t) {
+  const int c = (f >> 2) & 31, h = f >> 7, sp = f & 3;
+  const int mm = t >> 4, t16 = t & 15, gs = (t16 & 7) >> 2, hi = t16 >> 3, wq = t & 3;
+  const int slot = 4 * hi + (wq == 1 ? 2 : (wq == 2 ? 1 : wq));
+  return ((((h * 4 + sp) * 2 + mm) * 64) + c + 32 * gs) * 8 + slot;
+}
 
 __device__ __forceinline__ int64_t seat_of(int64_t slot, const StageArgs& a) {
   const int64_t page = slot / a.block_size;
@@ -93,6 +121,12 @@ __global__ __launch_bounds__(256) void stage_update_kernel(StageArgs a) {
     const int64_t dst = (seat * a.num_kv_heads + h) * kHeadDim + f;
     a.stage_k[dst] = yk;
     a.stage_v[dst] = yv;
+    if (a.kimg != nullptr) {
+      const int prow = (int)(seat % a.block_size);
+      const int64_t img = ((seat / a.block_size) * (a.block_size / 32) + prow / 32) * a.num_kv_heads + h;
+      a.kimg[img * kImgHalfs + kimg_offset(f, prow & 31)] = (_Float16)yk;
+      a.vimg[img * kImgHalfs + vimg_offset(f, prow & 31)] = (_Float16)yv;
+    }
   }
 }
 
@@ -108,7 +142,8 @@ extern "C" int oscar_staging_write(const void* key_bf16, const void* value_bf16,
                                    int32_t block_size, int32_t stage_rows, int32_t sink_eff,
                                    int32_t recent, const float* rot_k, const float* rot_v,
                                    float* stage_k, float* stage_v, int64_t* stage_owner,
-                                   int32_t* seat_winner, hipStream_t stream) {
+                                   int32_t* seat_winner, void* stage_k_image, void* stage_v_image,
+                                   hipStream_t stream) {
   if (head_size != kHeadDim) return kErrUnsupportedHeadDim;
   if (num_tokens < 0 || num_requests < 0 || num_kv_heads <= 0 || block_size <= 0 || stage_rows <= 0 ||
       sink_eff < 0 || recent < 0 || token_stride < (int64_t)num_kv_heads * kHeadDim)
@@ -117,10 +152,13 @@ extern "C" int oscar_staging_write(const void* key_bf16, const void* value_bf16,
   if (!key_bf16 || !value_bf16 || !slot_mapping || !query_start_loc || !seq_lens || !rot_k || !rot_v ||
       !stage_k || !stage_v || !stage_owner || !seat_winner)
     return kErrInvalidArgument;
+  if ((stage_k_image == nullptr) != (stage_v_image == nullptr)) return kErrInvalidArgument;
+  if (stage_k_image != nullptr && block_size % 32 != 0) return kErrUnsupportedGeometry;
   StageArgs a{static_cast<const uint16_t*>(key_bf16), static_cast<const uint16_t*>(value_bf16),
               token_stride, slot_mapping, num_tokens, query_start_loc, seq_lens, num_requests,
               num_kv_heads, block_size, stage_rows, sink_eff, recent, rot_k, rot_v, stage_k, stage_v,
-              stage_owner, seat_winner};
+              stage_owner, seat_winner, static_cast<_Float16*>(stage_k_image),
+              static_cast<_Float16*>(stage_v_image)};
   hipLaunchKernelGGL(stage_winner_kernel, dim3((num_tokens + 255) / 256), dim3(256), 0, stream, a);
   if (hipGetLastError() != hipSuccess) return kErrLaunch;
   hipLaunchKernelGGL(stage_update_kernel, dim3(num_tokens), dim3(kHeadDim), 0, stream, a);

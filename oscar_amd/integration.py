@@ -6,6 +6,7 @@ whole cache blocks.  Per OSCAR layer the fixed buffers here are
   * R_k, R_v and their transposes, fp32       4 * D^2 * 4
   * the two MFMA rotation operands             2 * oscar_rotation_operand_bytes(D)
   * the FP32 window arena                      rows * bs * (2 * Hk * D * 4 + 8)
+  * its fp16 MFMA operand images (K and V)     rows * bs * 2 * Hk * D * 2
   * the arena's seat-winner scratch            rows * bs * 4
 and, once per device, the split-decode workspace of the largest batch.
 """
@@ -39,13 +40,14 @@ def fixed_bytes_per_layer(head_dim: int, num_kv_heads: int, block_size: int, sin
     fixed = 4 * head_dim * head_dim * 4 + 2 * ROTATION_OPERAND_BYTES
     if window:
         rows = arena_rows(block_size, sink, recent, staging)
-        fixed += rows * block_size * (2 * num_kv_heads * head_dim * 4 + 8 + 4)
+        fixed += rows * block_size * (2 * num_kv_heads * head_dim * 4 + 2 * num_kv_heads * head_dim * 2 + 8 + 4)
     return fixed
 
 
 DECODE_TILE = 32                       # history tokens per decode tile
 DECODE_ROWS = 32                       # (query, head) rows per partial
 DECODE_PARTIAL_FLOATS = DECODE_ROWS * 256 + 2 * DECODE_ROWS
+DECODE_LAUNCH_REQUESTS = 128           # requests carried in one launch's kernel arguments
 
 
 def decode_tiles_per_split(max_requests: int, num_kv_heads: int, max_history: int) -> int:
@@ -67,7 +69,8 @@ def decode_workspace_bytes(max_requests: int, num_kv_heads: int, num_heads: int,
     tiles = -(-max_history // DECODE_TILE) if max_history > 0 else 0
     splits = -(-tiles // tps)
     row_tiles = -(-(max_query_len * (num_heads // num_kv_heads)) // DECODE_ROWS)
-    return max_requests * num_kv_heads * splits * row_tiles * DECODE_PARTIAL_FLOATS * 4
+    chunk = min(max_requests, DECODE_LAUNCH_REQUESTS)      # requests per launch share one workspace
+    return chunk * num_kv_heads * splits * row_tiles * DECODE_PARTIAL_FLOATS * 4
 
 
 def kv_block_bytes(block_size: int, num_kv_heads: int, slot_width: int, layers: int) -> int:

@@ -41,7 +41,7 @@ SIGNATURES = {
                                             _c_i32, _c_f32, _c_p, _c_p]),
     "oscar_staging_write": (_c_i32, [_c_p, _c_p, _c_i64, _c_p, _c_i32, _c_p, _c_p, _c_i32, _c_i32,
                                      _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p,
-                                     _c_p, _c_p, _c_p]),
+                                     _c_p, _c_p, _c_p, _c_p, _c_p]),
 }
 
 STATUS = {

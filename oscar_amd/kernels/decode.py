@@ -3,18 +3,22 @@
 Mirrors the reference seam ``oscar_paged_attention_triton(q, k, v, kc, vc, bt,
 qsl, seqs, scale, stage=None)`` (oscar_ascend/kernels/paged_attention.py:272-360):
 same arguments and meaning, rotated-domain fp32 inputs, rotated-V-domain fp32
-output [n, Hq, D].  ``qsl``/``seqs`` are host lists (the reference's
+output [n, Hq, D].  ``stage`` is the arena (stage_k, stage_v, owner[, k_image,
+v_image]); the kernel reads the window through the owner tags and the fp16
+operand images, which are built from the fp32 arena when not given.  ``qsl``/``seqs`` are host lists (the reference's
 metadata_batch_lists); they are validated exactly like the reference's
-query_layout (paged_attention.py:20-38) and uploaded once per call.
+query_layout (paged_attention.py:20-38) and handed to the library as host
+arrays, which it places in the kernel arguments.
 """
 from __future__ import annotations
 
+import ctypes
 import itertools
 
 import torch
 
 from ..format import check_d
-from . import _lib
+from . import _lib, staging
 from .quant import cache_geometry
 
 MAX_QUERY_LEN = 16          # rows per request <= 16 tokens x group (backend.py:277)
@@ -76,18 +80,27 @@ def plan(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None, out=None,
     if bt.ndim != 2:
         raise ValueError("block table must be [requests, pages]")
     bt = bt.to(device=dev, dtype=torch.int32).contiguous()
-    meta = torch.tensor(list(qsl) + list(seqs), dtype=torch.int32).to(dev, non_blocking=True)
-    qstart, seq_t = meta[:len(qsl)], meta[len(qsl):]
+    # Request layout as host int32 arrays: the library copies it into the
+    # kernel arguments (no device metadata round trip).
+    qstart = (ctypes.c_int32 * len(qsl))(*[int(x) for x in qsl])
+    seq_t = (ctypes.c_int32 * max(len(seqs), 1))(*[int(x) for x in seqs])
     bs, pages, kst, vst = cache_geometry(kc, vc)
     if stage is not None:
-        sk, sv, owner = stage
-        if sk.shape[1] != bs:
+        owner = stage[2]
+        if owner.shape[1] != bs:
             raise ValueError("staging arena block size must equal the cache block size")
-        sk, sv = sk.float().contiguous(), sv.float().contiguous()
         owner = owner.to(torch.int64).contiguous()
         rows = owner.shape[0]
+        if len(stage) >= 5 and stage[3] is not None:
+            kimg, vimg = stage[3], stage[4]
+        else:
+            kimg, vimg = staging.stage_images(stage[0], stage[1])
+        want = staging.image_shape(rows, bs, hk)
+        if tuple(kimg.shape) != want or tuple(vimg.shape) != want or kimg.dtype != torch.float16 \
+                or vimg.dtype != torch.float16 or not (kimg.is_contiguous() and vimg.is_contiguous()):
+            raise ValueError(f"staging operand images must be contiguous fp16 {want}")
     else:
-        sk = sv = owner = None
+        owner = kimg = vimg = None
         rows = 0
     B = len(lengths)
     if bs % 32:
@@ -97,10 +110,10 @@ def plan(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None, out=None,
     if out is None:
         out = torch.empty(n, hq, d, dtype=torch.float32, device=dev)
     args = (_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), n, hq, hk, d, _lib.ptr(kc), _lib.ptr(vc), bs,
-            pages, *kst, *vst, _lib.ptr(bt), bt.stride(0), bt.shape[1], _lib.ptr(qstart),
-            _lib.ptr(seq_t), B, max_q, max_hist, _lib.ptr(sk), _lib.ptr(sv), _lib.ptr(owner), rows,
+            pages, *kst, *vst, _lib.ptr(bt), bt.stride(0), bt.shape[1], ctypes.addressof(qstart),
+            ctypes.addressof(seq_t), B, max_q, max_hist, _lib.ptr(owner), _lib.ptr(kimg), _lib.ptr(vimg), rows,
             float(scale), int(tiles_per_split), _lib.ptr(out), _lib.ptr(ws), ws.numel())
-    return DecodePlan(args, out, [q, k, v, kc, vc, bt, meta, sk, sv, owner, ws])
+    return DecodePlan(args, out, [q, k, v, kc, vc, bt, qstart, seq_t, owner, kimg, vimg, ws])
 
 
 def paged_attention(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None) -> torch.Tensor:

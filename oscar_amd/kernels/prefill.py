@@ -33,7 +33,7 @@ def prefill_continuation(q_rot, k_rot, v_rot, kc, vc, bt_row, cached_len: int, s
     bt = bt_row.to(device=dev, dtype=torch.int32).contiguous().reshape(-1)
     bs, pages, kst, vst = cache_geometry(kc, vc)
     if stage is not None:
-        sk, sv, owner = stage
+        sk, sv, owner = stage[:3]
         sk, sv = sk.float().contiguous(), sv.float().contiguous()
         owner = owner.to(torch.int64).contiguous()
         rows = owner.shape[0]

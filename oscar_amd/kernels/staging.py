@@ -20,9 +20,52 @@ def arena_geometry(bs: int, sink: int, recent: int, staging: int):
     return sink_eff, sink_pages, tail_pages, rows
 
 
+IMAGE_HALFS = 16 * 64 * 8      # one operand image of a 32-token tile: 16 blocks x 64 lanes x 8
+
+
+def _k_image_order() -> torch.Tensor:
+    """Feature at (g, m, u) of the K image: 128g + 16(m // 2) + 4(m % 2) + u // 2 + 8(u % 2)."""
+    g = torch.arange(2).view(2, 1, 1)
+    m = torch.arange(16).view(1, 16, 1)
+    u = torch.arange(8).view(1, 1, 8)
+    return (128 * g + 16 * (m // 2) + 4 * (m % 2) + u // 2 + 8 * (u % 2)).reshape(-1)
+
+
+def _v_image_tokens() -> torch.Tensor:
+    """Token at (mm, gs, u) of the V image: 16mm + 4gs + (0, 2, 1, 3, 8, 10, 9, 11)[u]."""
+    order = torch.tensor([0, 2, 1, 3, 8, 10, 9, 11])
+    mm = torch.arange(2).view(2, 1, 1)
+    gs = torch.arange(2).view(1, 2, 1)
+    return (16 * mm + 4 * gs + order.view(1, 1, 8)).reshape(-1)
+
+
+def image_shape(rows: int, bs: int, hk: int) -> tuple:
+    return (rows, bs // 32, hk, IMAGE_HALFS)
+
+
+def stage_images(stage_k: torch.Tensor, stage_v: torch.Tensor):
+    """fp16 operand images of a whole arena (the layout oscar_staging_write
+    maintains incrementally): K [rows][bs/32][Hk][m][lane = t + 32g][slot],
+    V [rows][bs/32][Hk][h][sp][mm][lane = c + 32gs][slot]."""
+    rows, bs, hk, d = stage_k.shape
+    if d != 256 or bs % 32:
+        raise ValueError("operand images need D = 256 and a block size that is a multiple of 32")
+    T = bs // 32
+    dev = stage_k.device
+    x = stage_k.view(rows, T, 32, hk, d).to(torch.float16)[..., _k_image_order().to(dev)]
+    x = x.view(rows, T, 32, hk, 2, 16, 8).permute(0, 1, 3, 5, 4, 2, 6)      # [r, T, hk, m, g, t, u]
+    kimg = x.reshape(rows, T, hk, IMAGE_HALFS).contiguous()
+    y = stage_v.view(rows, T, 32, hk, d).to(torch.float16).permute(0, 1, 3, 4, 2)  # [r, T, hk, f, tok]
+    y = y[..., _v_image_tokens().to(dev)]                                    # [r, T, hk, f, (mm, gs, u)]
+    y = y.reshape(rows, T, hk, 2, 32, 4, 2, 2, 8)                           # f = (h, c, sp)
+    y = y.permute(0, 1, 2, 3, 5, 6, 7, 4, 8)                                 # [r, T, hk, h, sp, mm, gs, c, u]
+    vimg = y.reshape(rows, T, hk, IMAGE_HALFS).contiguous()
+    return kimg, vimg
+
+
 def staging_write(key, value, slot_mapping, qsl_dev, seq_dev, num_requests: int, num_kv_heads: int,
                   head_size: int, block_size: int, sink_eff: int, recent: int, R_k, R_v,
-                  stage_k, stage_v, owner, winner) -> None:
+                  stage_k, stage_v, owner, winner, k_image=None, v_image=None) -> None:
     N = slot_mapping.shape[0]
     if N == 0 or num_requests == 0:
         return
@@ -36,4 +79,5 @@ def staging_write(key, value, slot_mapping, qsl_dev, seq_dev, num_requests: int,
     _lib.call("oscar_staging_write", _lib.ptr(kr), _lib.ptr(vr), kr.stride(0), _lib.ptr(slots), N,
               _lib.ptr(qsl_dev), _lib.ptr(seq_dev), num_requests, num_kv_heads, head_size, block_size,
               owner.shape[0], sink_eff, recent, _lib.ptr(R_k), _lib.ptr(R_v), _lib.ptr(stage_k),
-              _lib.ptr(stage_v), _lib.ptr(owner), _lib.ptr(winner), _lib.stream_handle(key.device))
+              _lib.ptr(stage_v), _lib.ptr(owner), _lib.ptr(winner), _lib.ptr(k_image), _lib.ptr(v_image),
+              _lib.stream_handle(key.device))

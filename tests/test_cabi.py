@@ -66,8 +66,10 @@ def test_size_queries(lib):
     assert lib.oscar_rotation_operand_bytes(128) == 0
     assert lib.oscar_paged_decode_workspace_bytes(0, 1, 6, 4, 100, 0) == 0
     assert lib.oscar_paged_decode_workspace_bytes(1, 2, 5, 4, 100, 0) == 0     # Hq % Hk
+    assert lib.oscar_paged_decode_workspace_bytes(1, 1, 6, 4, 100, 257) == 0   # tiles per split cap
     for args in [(1, 1, 6, 4, 24579, 0), (8, 1, 6, 4, 6000, 0), (3, 2, 12, 16, 131072, 0),
-                 (1, 1, 6, 1, 0, 0), (64, 4, 32, 16, 1 << 20, 0), (2, 1, 6, 4, 24579, 4)]:
+                 (1, 1, 6, 1, 0, 0), (64, 4, 32, 16, 1 << 20, 0), (2, 1, 6, 4, 24579, 4),
+                 (300, 1, 6, 4, 4096, 0), (129, 2, 12, 2, 100, 8)]:
         want = integration.decode_workspace_bytes(*args[:5], tiles_per_split=args[5])
         assert lib.oscar_paged_decode_workspace_bytes(*args) == want, args
 

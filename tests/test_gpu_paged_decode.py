@@ -77,6 +77,15 @@ def test_concurrent_requests_shared_pool(device):
     run_case(case, device)
 
 
+def test_more_requests_than_one_launch_carries(device):
+    # 150 requests: the library launches them in two chunks that share one workspace.
+    g = torch.Generator().manual_seed(11)
+    hist = torch.randint(0, 400, (150,), generator=g).tolist()
+    qlens = torch.randint(1, 5, (150,), generator=g).tolist()
+    case = decode_case(hist, qlens, bs=32, seed=12, pool_pages=2400, sink=32, recent=32, staging=64)
+    run_case(case, device)
+
+
 def test_window_disabled_matches_pure_int2(device):
     case = decode_case([3000], [4], seed=8, window=False)
     run_case(case, device, with_stage=False)

@@ -31,7 +31,12 @@ def _gpu_arena(arena, device):
     sv = torch.zeros_like(sk)
     owner = torch.full(arena.owner.shape, -1, dtype=torch.int64, device=device)
     winner = torch.full(arena.owner.shape, -1, dtype=torch.int32, device=device)
-    return sk, sv, owner, winner
+    kimg = vimg = None
+    if arena.bs % 32 == 0:
+        shape = staging.image_shape(arena.rows, arena.bs, arena.stage_k.shape[2])
+        kimg = torch.zeros(shape, dtype=torch.float16, device=device)
+        vimg = torch.zeros(shape, dtype=torch.float16, device=device)
+    return sk, sv, owner, winner, kimg, vimg
 
 
 def _write_both(arena, gpu, key, value, md, Rk, Rv, device):
@@ -39,10 +44,10 @@ def _write_both(arena, gpu, key, value, md, Rk, Rv, device):
     qsl, seqs = md.query_start_loc.tolist(), md.seq_lens.tolist()
     B = len(seqs)
     meta = torch.tensor(qsl + seqs, dtype=torch.int32, device=device)
-    sk, sv, owner, winner = gpu
+    sk, sv, owner, winner, kimg, vimg = gpu
     staging.staging_write(key.to(device), value.to(device), md.slot_mapping.to(device), meta[:B + 1],
                           meta[B + 1:], B, key.shape[1], D, arena.bs, arena.sink_eff, arena.recent,
-                          Rk.to(device), Rv.to(device), sk, sv, owner, winner)
+                          Rk.to(device), Rv.to(device), sk, sv, owner, winner, kimg, vimg)
 
 
 @pytest.mark.parametrize("bs,sink,recent,staging_tokens", [(4, 4, 4, 8), (16, 16, 32, 64), (128, 128, 256, 8192)])
@@ -72,8 +77,12 @@ def test_window_write_matches_oracle_over_steps(device, bs, sink, recent, stagin
         md = metadata(slots, qsl, seqs, bt)
         _write_both(arena, gpu, k, v, md, Rk, Rv, device)
         torch.cuda.synchronize()
-        sk, sv, owner, winner = (t.cpu() for t in gpu)
+        sk, sv, owner, winner = (t.cpu() for t in gpu[:4])
         assert torch.equal(owner, arena.owner), f"owner tags differ at step {i}"
+        if gpu[4] is not None:
+            # The fp16 operand images track the fp32 arena exactly (same RNE cast).
+            kref, vref = staging.stage_images(gpu[0], gpu[1])
+            assert torch.equal(gpu[4], kref) and torch.equal(gpu[5], vref), f"operand images differ at step {i}"
         assert (winner == -1).all()
         live = arena.owner >= 0
         for got, want in ((sk, arena.stage_k), (sv, arena.stage_v)):
