@@ -47,15 +47,19 @@ def fixed_bytes_per_layer(head_dim: int, num_kv_heads: int, block_size: int, sin
 DECODE_TILE = 32                       # history tokens per decode tile
 DECODE_ROWS = 32                       # (query, head) rows per partial
 DECODE_PARTIAL_FLOATS = DECODE_ROWS * 256 + 2 * DECODE_ROWS
-DECODE_LAUNCH_REQUESTS = 128           # requests carried in one launch's kernel arguments
+DECODE_LAUNCH_ITEMS = 128              # (request, kv head) items carried in one launch's kernel arguments
+DECODE_MAX_SPLITS = 1023               # history splits per item (the fresh-token partial makes 1024)
+DECODE_MAX_TILES_PER_SPLIT = 256
 
 
 def decode_tiles_per_split(max_requests: int, num_kv_heads: int, max_history: int) -> int:
     """The library's default split length (in tiles) for this batch shape."""
     tiles = -(-max_history // DECODE_TILE) if max_history > 0 else 0
     work = tiles * max_requests * num_kv_heads
-    tps = 8
+    tps = 4
     while tps < 64 and work // tps > 1024:
+        tps *= 2
+    while tps < DECODE_MAX_TILES_PER_SPLIT and -(-tiles // tps) > DECODE_MAX_SPLITS:
         tps *= 2
     return tps
 
@@ -64,13 +68,14 @@ def decode_workspace_bytes(max_requests: int, num_kv_heads: int, num_heads: int,
                            max_history: int, tiles_per_split: int = 0) -> int:
     """Same value as oscar_paged_decode_workspace_bytes (no library needed):
     one fp32 partial (32 rows x 256 + max + sum) per (request, kv head,
-    split, row tile)."""
+    history split or the fresh-token split, row tile)."""
     tps = tiles_per_split or decode_tiles_per_split(max_requests, num_kv_heads, max_history)
     tiles = -(-max_history // DECODE_TILE) if max_history > 0 else 0
     splits = -(-tiles // tps)
     row_tiles = -(-(max_query_len * (num_heads // num_kv_heads)) // DECODE_ROWS)
-    chunk = min(max_requests, DECODE_LAUNCH_REQUESTS)      # requests per launch share one workspace
-    return chunk * num_kv_heads * splits * row_tiles * DECODE_PARTIAL_FLOATS * 4
+    per_launch = DECODE_LAUNCH_ITEMS // num_kv_heads         # requests per launch share one workspace
+    chunk = min(max_requests, per_launch)
+    return chunk * num_kv_heads * (splits + 1) * row_tiles * DECODE_PARTIAL_FLOATS * 4
 
 
 def kv_block_bytes(block_size: int, num_kv_heads: int, slot_width: int, layers: int) -> int:
