@@ -43,9 +43,9 @@
 //    fp16; a tile with a V scale above 4094 raises it eagerly), and the first
 //    raise of a row needs no rescale.  The 4 wavefronts agree on a common max
 //    in LDS and reduce-scatter their O^T fragments in two LDS rounds: wave w
-//    ends with features 64w .. 64w + 63 of every row and writes them straight
-//    from its registers into the split's partial [32 rows][256] + m[32] +
-//    l[32] (fp32, row-major).
+//    ends with features 64w .. 64w + 63 of every row, transposes them through
+//    LDS and writes whole row segments of the split's partial [32 rows][256]
+//    + m[32] + l[32] (fp32, row-major).
 //  * workgroup S: the step's own new tokens in exact fp32 (row (token j,
 //    head) against new tokens 0 .. j), written as one more partial.
 // merge kernel: one 256-thread block per (output row, feature quarter) of an
@@ -518,12 +518,14 @@ __device__ __forceinline__ void rs_recv1_send2(floatx16 (&acc)[8], float f4, flo
     }
 }
 
-// Final round: add the partner's copy of the kept registers and write this
-// wave's 64 features of every valid row: feature 128H + 32jq + 16g + 4i + sp
-// is register 4jq + i of tile 4H + sp.
+// Final round: add the partner's copy of the kept registers and stage this
+// wave's 64 features of every row, [row][64 + 4 pad] fp32, in LDS (register
+// 4jq + i of tile 4H + sp is local feature 32(jq - 2J) + 16g + 4i + sp).
+constexpr int kTRow = 68;
+constexpr int kTFloats = kRows * kTRow;
+
 template <int W>
-__device__ __forceinline__ void rs_recv2_write(floatx16 (&acc)[8], const float* cb, float* part, int lane,
-                                               int nrow) {
+__device__ __forceinline__ void rs_recv2_stage(floatx16 (&acc)[8], const float* cb, float* tb, int lane) {
   constexpr int H = W >> 1, J = W & 1;
   const float* src = cb + 4 * kR1Floats + (W ^ 1) * kR2Floats;
   const int g = lane >> 5, col = lane & 31;
@@ -536,17 +538,14 @@ __device__ __forceinline__ void rs_recv2_write(floatx16 (&acc)[8], const float* 
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[4 * H + tt][r0 + i] += v[i];
     }
-  if (col < nrow) {
-    float* row = part + col * kHeadDim + 128 * H + 16 * g;
+  float* row = tb + W * kTFloats + col * kTRow + 16 * g;
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const int jq = 2 * J + jj;
+  for (int jj = 0; jj < 2; ++jj) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * jq + i;
-        *reinterpret_cast<floatx4*>(row + 32 * jq + 4 * i) =
-            floatx4{acc[4 * H][r], acc[4 * H + 1][r], acc[4 * H + 2][r], acc[4 * H + 3][r]};
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * (2 * J + jj) + i;
+      *reinterpret_cast<floatx4*>(row + 32 * jj + 4 * i) =
+          floatx4{acc[4 * H][r], acc[4 * H + 1][r], acc[4 * H + 2][r], acc[4 * H + 3][r]};
     }
   }
 }
@@ -565,10 +564,12 @@ __device__ void fresh_partial(const DecodeArgs& a, const ItemInfo& it, int item,
   const int h = kvh * a.group + (row - j * a.group);
   floatx4 x[8];
   {
+    // Thread (r, c) owns features 32k + 4c .. +3: each load and store
+    // instruction covers whole 128-byte row segments.
     const floatx4* src = reinterpret_cast<const floatx4*>(a.q + ((int64_t)(it.qa + j) * a.num_heads + h) *
-                                                          kHeadDim + 32 * c);
+                                                          kHeadDim + 4 * c);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) x[k] = src[k];
+    for (int k = 0; k < 8; ++k) x[k] = src[8 * k];
   }
   // New keys and values of the request: [nq][2][64 float4], 8 per thread at most.
   floatx4 kv[kMaxFresh * 128 / 256];
@@ -594,11 +595,11 @@ __device__ void fresh_partial(const DecodeArgs& a, const ItemInfo& it, int item,
   for (int i = 0; i < kMaxFresh; ++i) {
     sc[i] = -__builtin_inff();
     if (i < nq) {
-      const floatx4* kr = reinterpret_cast<const floatx4*>(&F.kf[i][32 * c]);
+      const floatx4* kr = reinterpret_cast<const floatx4*>(&F.kf[i][4 * c]);
       float d = 0.f;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        const floatx4 kk = kr[k];
+        const floatx4 kk = kr[8 * k];
         d = fmaf(x[k][0], kk[0], d);
         d = fmaf(x[k][1], kk[1], d);
         d = fmaf(x[k][2], kk[2], d);
@@ -622,16 +623,16 @@ __device__ void fresh_partial(const DecodeArgs& a, const ItemInfo& it, int item,
     if (i < nq) {
       const float p = (i <= j) ? exp2f(sc[i] - mx) : 0.f;
       l += p;
-      const floatx4* vr = reinterpret_cast<const floatx4*>(&F.vf[i][32 * c]);
+      const floatx4* vr = reinterpret_cast<const floatx4*>(&F.vf[i][4 * c]);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) o[k] += p * vr[k];
+      for (int k = 0; k < 8; ++k) o[k] += p * vr[8 * k];
     }
   }
   if (valid) {
     float* part = a.ws + item_index(a, item, a.max_splits, rt) * kPartialFloats;
-    float* dst = part + r * kHeadDim + 32 * c;
+    float* dst = part + r * kHeadDim + 4 * c;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) reinterpret_cast<floatx4*>(dst)[k] = o[k];
+    for (int k = 0; k < 8; ++k) reinterpret_cast<floatx4*>(dst)[8 * k] = o[k];
     if (c == 0) {
       part[kPartO + r] = mx;
       part[kPartO + kRows + r] = l;
@@ -831,13 +832,24 @@ __global__ __launch_bounds__(256) void paged_decode_split_kernel(DecodeArgs a) {
     default: rs_recv1_send2<3>(st.acc, f4, off, cb, lane); break;
   }
   __syncthreads();
+  // Round 1's buffers are free now: each wave stages its [32][64] block
+  // there and writes whole 256-byte row segments (16 lanes per row).
+  float* tb = cb;
+  switch (w) {
+    case 0: rs_recv2_stage<0>(st.acc, cb, tb, lane); break;
+    case 1: rs_recv2_stage<1>(st.acc, cb, tb, lane); break;
+    case 2: rs_recv2_stage<2>(st.acc, cb, tb, lane); break;
+    default: rs_recv2_stage<3>(st.acc, cb, tb, lane); break;
+  }
+  wave_sync_lds();
   const int nrow = min(kRows, rows - rt * kRows);
   float* part = a.ws + item_index(a, item, split, rt) * kPartialFloats;
-  switch (w) {
-    case 0: rs_recv2_write<0>(st.acc, cb, part, lane, nrow); break;
-    case 1: rs_recv2_write<1>(st.acc, cb, part, lane, nrow); break;
-    case 2: rs_recv2_write<2>(st.acc, cb, part, lane, nrow); break;
-    default: rs_recv2_write<3>(st.acc, cb, part, lane, nrow); break;
+#pragma unroll
+  for (int s4 = 0; s4 < kRows / 4; ++s4) {
+    const int row = 4 * s4 + (lane >> 4);
+    if (row < nrow)
+      *reinterpret_cast<floatx4*>(part + row * kHeadDim + 64 * w + 4 * (lane & 15)) =
+          *reinterpret_cast<const floatx4*>(tb + w * kTFloats + row * kTRow + 4 * (lane & 15));
   }
   if (w == 0 && lane < nrow) {
     float lsum = 0.f;
@@ -857,7 +869,7 @@ __global__ __launch_bounds__(256) void paged_decode_split_kernel(DecodeArgs a) {
 // (thread per partial) and the block's 64-feature slice of every partial row
 // (thread: partial group t / 16, features 4 * (t % 16) .. +3 of the quarter).
 constexpr int kMergeGroups = 16;                 // partial groups per block
-constexpr int kMergeBatch = 8;                   // partial loads per thread per round
+constexpr int kMergeBatch = 16;                  // partial loads per thread per round
 constexpr int kMaxPartials = kMaxSplits + 1;
 
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
