@@ -6,7 +6,18 @@
 // 128 fp32 registers, so every per-vector reduction is lane-local plus one
 // exchange with lane l ^ 32.  That is exactly the fp32 accumulator layout of
 // a 32x32 MFMA tile whose columns are tokens, which the fused entry point
-// uses for the 256x256 rotation (bf16 hi + lo split of R, two passes).
+// uses for the 256x256 rotation (bf16 hi + lo split of R, two passes; the
+// operand streams through a 4-deep LDS ring filled by direct-to-LDS loads).
+//
+// Clip threshold (the idx-th smallest |x| of a vector, i.e. its kk-th largest
+// with kk = 256 - idx) without sorting: a 64-bucket histogram of |x| keyed on
+// the float bits (bucket = key(max|x|) - key(|x|), key = bits >> S, S = 18:
+// 1/32 octave per bucket over two octaves) built with LDS atomics gives the
+// bucket holding the answer and its rank j inside that bucket; the bucket's
+// few values are gathered into small per-lane LDS lists and the j-th largest
+// of them is taken exactly (ties counted).  Vectors whose answer lies outside
+// the histogram's range or whose bucket overflows the lists use a bitwise
+// radix select instead (exact, slow, rare).
 //
 // Quantization is bit-exact with the reference's fp32 formula
 //   q = clamp(floor((x - zero) / scale + 0.5), 0, 3)
@@ -50,6 +61,124 @@ __device__ float select_abs_rank(const float (&v)[kPerLane], int idx) {
   return __uint_as_float(prefix);
 }
 
+// Per-wave LDS of the threshold search: 32 token histograms (64 buckets + one
+// bucket for everything below the range; stride 65 words keeps the tokens of
+// one wave on different banks) and one candidate list per lane.
+constexpr int kHistBuckets = 64;
+constexpr int kHistStride = kHistBuckets + 1;
+constexpr int kListCap = 8;
+constexpr int kListStride = kListCap + 1;          // + one slot that absorbs non-candidates
+struct SelLds {
+  uint32_t hist[32 * kHistStride];
+  uint32_t list[64 * kListStride];
+};
+
+__device__ __forceinline__ void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// kk-th largest |x| (kk = 256 - idx) of the 256 values held by this lane and
+// its partner, as float bits; amax_bits = bits of max |x| over both lanes.
+__device__ uint32_t select_clip_bits(const float (&v)[kPerLane], int idx, uint32_t amax_bits, SelLds& L,
+                                     int lane) {
+  const uint32_t kk = (uint32_t)(kHeadDim - idx);
+  const int t = lane & 31, g = lane >> 5;
+  const int S = kk <= 40 ? 18 : 20;          // 1/32 octave per bucket (2 octaves); coarser for deep ranks
+  uint4* hz = reinterpret_cast<uint4*>(L.hist);
+  for (int i = lane; i < 32 * kHistStride / 4; i += 64) hz[i] = uint4{0u, 0u, 0u, 0u};
+  wave_sync_lds();
+  uint32_t* H = L.hist + t * kHistStride;
+  const uint32_t kh = amax_bits >> S;
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) {
+    const uint32_t key = __builtin_amdgcn_ubfe(__float_as_uint(v[i]), S, 31 - S);
+    const uint32_t b = min(kh - key, (uint32_t)kHistBuckets);
+    atomicAdd(&H[b], 1u);
+  }
+  wave_sync_lds();
+
+  // Bucket b* where the count from the top reaches kk; lane g scans buckets
+  // 32g .. 32g + 31.
+  uint32_t cnt[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) cnt[i] = H[32 * g + i];
+  uint32_t tot = 0;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) tot += cnt[i];
+  // (the exchange runs on every lane: a shuffle reads only active lanes)
+  const uint32_t tot0 = (uint32_t)__shfl((int)tot, t, 64);
+  uint32_t run = g ? tot0 : 0u;
+  int bf = -1;
+  uint32_t above = 0;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    if (bf < 0 && run + cnt[i] >= kk) {
+      bf = 32 * g + i;
+      above = run;
+    }
+    run += cnt[i];
+  }
+  const int b0 = __shfl(bf, t, 64), b1 = __shfl(bf, t + 32, 64);
+  const uint32_t a0 = (uint32_t)__shfl((int)above, t, 64), a1 = (uint32_t)__shfl((int)above, t + 32, 64);
+  const int bstar = b0 >= 0 ? b0 : b1;
+  const uint32_t ab = b0 >= 0 ? a0 : a1;
+  const uint32_t keystar = kh - (uint32_t)bstar;
+  bool fb = bstar < 0 || keystar == 0;
+
+  // Gather bucket b*'s values: every value is written at the lane's next free
+  // slot, which only advances on a match (capped at the absorbing slot).
+  uint32_t* mine = L.list + lane * kListStride;
+  uint32_t n = 0;
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) {
+    const uint32_t u = __float_as_uint(v[i]) & 0x7FFFFFFFu;
+    mine[min(n, (uint32_t)kListCap)] = u;
+    n += (u >> S) == keystar ? 1u : 0u;
+  }
+  wave_sync_lds();
+  const uint32_t n0 = (uint32_t)__shfl((int)n, t, 64), n1 = (uint32_t)__shfl((int)n, t + 32, 64);
+  fb = fb || n0 > kListCap || n1 > kListCap;
+  uint32_t c[2 * kListCap];
+  const uint32_t* l0 = L.list + t * kListStride;
+  const uint32_t* l1 = L.list + (t + 32) * kListStride;
+#pragma unroll
+  for (int i = 0; i < kListCap; ++i) {
+    c[i] = (uint32_t)i < n0 ? l0[i] : 0u;
+    c[kListCap + i] = (uint32_t)i < n1 ? l1[i] : 0u;
+  }
+  // j-th largest of the candidates (j = kk - above >= 1), ties counted.
+  uint32_t rem = kk - ab, prev = 0xFFFFFFFFu, res = 0u;
+  if (fb) rem = 0;
+#pragma unroll 1
+  for (int it = 0; it <= 2 * kListCap && __ballot(rem > 0); ++it) {
+    uint32_t m = 0u;
+#pragma unroll
+    for (int i = 0; i < 2 * kListCap; ++i) m = max(m, c[i] < prev ? c[i] : 0u);
+    uint32_t ce = 0u;
+#pragma unroll
+    for (int i = 0; i < 2 * kListCap; ++i) ce += (c[i] == m) ? 1u : 0u;
+    if (rem > 0) {
+      if (m == 0u) {
+        fb = true;
+        rem = 0;
+      } else if (ce >= rem) {
+        res = m;
+        rem = 0;
+      } else {
+        rem -= ce;
+        prev = m;
+      }
+    }
+  }
+  if (__ballot(fb)) {
+    const uint32_t r = __float_as_uint(select_abs_rank(v, idx));
+    if (fb) res = r;
+  }
+  return res;
+}
+
 // Smallest float >= d for a positive finite-or-infinite double d.
 __device__ __forceinline__ float round_up_f32(double d) {
   float f = (float)d;
@@ -63,7 +192,7 @@ struct QParams {
   uint32_t meta;          // scale fp16 bits | zero fp16 bits << 16
 };
 
-__device__ QParams vector_params(const float (&v)[kPerLane], int clip_idx) {
+__device__ QParams vector_params(const float (&v)[kPerLane], int clip_idx, SelLds& L, int lane) {
   float mx = v[0], mn = v[0];
 #pragma unroll
   for (int i = 1; i < kPerLane; ++i) {
@@ -74,7 +203,8 @@ __device__ QParams vector_params(const float (&v)[kPerLane], int clip_idx) {
   mn = fminf(mn, shfl_xor_f32(mn, 32));
   float thr = __builtin_inff();
   if (clip_idx >= 0) {
-    thr = select_abs_rank(v, clip_idx);
+    const uint32_t amax_bits = max(__float_as_uint(mx) & 0x7FFFFFFFu, __float_as_uint(mn) & 0x7FFFFFFFu);
+    thr = __uint_as_float(select_clip_bits(v, clip_idx, amax_bits, L, lane));
     mx = fminf(fmaxf(mx, -thr), thr);
     mn = fminf(fmaxf(mn, -thr), thr);
   }
@@ -154,6 +284,7 @@ __global__ __launch_bounds__(256) void quant_write_prerotated_kernel(
     const float* __restrict__ k_rot, const float* __restrict__ v_rot, int64_t n_tokens,
     int64_t token_stride, const int64_t* __restrict__ slots, CacheArgs c, int clip_k,
     int clip_v) {
+  __shared__ SelLds sel[4];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int head = blockIdx.y >> 1;
@@ -172,7 +303,7 @@ __global__ __launch_bounds__(256) void quant_write_prerotated_kernel(
     v[i + 2] = x[2];
     v[i + 3] = x[3];
   }
-  const QParams p = vector_params(v, side == 0 ? clip_k : clip_v);
+  const QParams p = vector_params(v, side == 0 ? clip_k : clip_v, sel[wave], lane);
   quantize_store(v, p, live ? slots[tok] : -1, head, side, half, c);
 }
 
@@ -185,18 +316,43 @@ __global__ __launch_bounds__(256) void quant_write_prerotated_kernel(
 //     e = 128*(lane >> 5) + 8*m + u                      (input feature)
 //     f = 128*((r >> 2) & 1) + 16*T + 4*(r >> 3) + (r & 3), r = lane & 31
 //   so that accumulator register i of tile T in lane l is feature
-//   128*(l >> 5) + 16*T + i of token (l & 31) — the per-lane layout above.
-// grid = (ceil(N / 256), Hk * 2), block = 512 (8 waves x 32 tokens); every
-// wave of a block shares the operand chunks streamed through LDS.
+//   128*(l >> 5) + 16*T + i of token (l & 31) -- the per-lane layout above.
+// grid = (ceil(N / 256), Hk * 2), block = 512 (8 waves x 32 tokens, two per
+// SIMD).  The 16 K-step chunks (16 KB each) stream through a 4-slot LDS ring
+// filled with global_load_lds_dwordx4: chunk m + 3 is requested while chunk m
+// is multiplied, into the slot chunk m - 1 left.  Each K step issues the 8
+// tiles' hi passes, then their lo passes, so no MFMA waits on the previous.
 // ---------------------------------------------------------------------------
-constexpr int kFusedWaves = 8;
+constexpr int kFusedWaves = 4;
 constexpr int kChunkBytes = 2 * 8 * 64 * 16;   // one K step: 2 passes x 8 tiles x 64 lanes x 16 B
+constexpr int kRing = 4;
+constexpr int kSteps = 16;
+constexpr int kDmaPerChunk = kChunkBytes / (kFusedWaves * 64 * 16);   // 2 per thread
+constexpr size_t kFusedLds = kFusedWaves * sizeof(SelLds) > kRing * kChunkBytes
+                                 ? kFusedWaves * sizeof(SelLds) : (size_t)kRing * kChunkBytes;
 
-__global__ __launch_bounds__(512) void quant_write_fused_kernel(
+// Workgroup barrier without a memory fence: __syncthreads() would also wait
+// for every outstanding global access (vmcnt(0)) and so drain the ring's
+// prefetches.  The asm memory clobber keeps the compiler from moving LDS
+// accesses across it; LDS visibility comes from the vmcnt waits above it
+// (direct-to-LDS loads count as complete once their data is in LDS) and
+// from the LDS reads' own completion before the next overwrite.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);                     // lgkmcnt(0): this wave's LDS reads done
+  asm volatile("s_barrier" ::: "memory");
+}
+
+// s_waitcnt vmcnt(n) with expcnt / lgkmcnt left at their maxima (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+__global__ __launch_bounds__(256, 2) void quant_write_fused_kernel(
     const uint16_t* __restrict__ key, const uint16_t* __restrict__ value, int64_t n_tokens,
     int64_t token_stride, const uint8_t* __restrict__ rot_k, const uint8_t* __restrict__ rot_v,
     const int64_t* __restrict__ slots, CacheArgs c, int clip_k, int clip_v) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2][kChunkBytes];
+  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];     // ring, then the selection buffers
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -218,47 +374,56 @@ __global__ __launch_bounds__(512) void quant_write_fused_kernel(
       xb[m] = __builtin_bit_cast(bf16x8, raw);
     }
   }
+  // Thread's share of a chunk: wave w copies 1 KB blocks 4w .. 4w + 3.
+  auto request = [&](int chunk) {
+#pragma unroll
+    for (int i = 0; i < kDmaPerChunk; ++i) {
+      const int blk = kDmaPerChunk * wave + i;
+      __builtin_amdgcn_global_load_lds(rop + (size_t)chunk * kChunkBytes + (blk * 64 + lane) * 16,
+                                       ring + (chunk % kRing) * kChunkBytes + blk * 1024, 16, 0, 0);
+    }
+  };
+  request(0);
+  request(1);
+  request(2);
 
   floatx16 acc[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) acc[t] = floatx16{};
 
-  // Stage K step 0.
-  const u32x4* gsrc = reinterpret_cast<const u32x4*>(rop);
-  constexpr int kVecPerChunk = kChunkBytes / 16;           // 1024 x 16 B
-  constexpr int kVecPerThread = kVecPerChunk / (kFusedWaves * 64);   // 2
-  u32x4 stage[kVecPerThread];
 #pragma unroll
-  for (int j = 0; j < kVecPerThread; ++j) stage[j] = gsrc[tid + j * kFusedWaves * 64];
+  for (int m = 0; m < kSteps; ++m) {
+    // This thread's copies of chunk m have landed (later chunks may still be
+    // in flight); after the barrier every thread's have, and chunk m - 1's
+    // slot is free for chunk m + 3.
+    if (m + 2 < kSteps) wait_vmcnt<2 * kDmaPerChunk>();
+    else if (m + 1 < kSteps) wait_vmcnt<kDmaPerChunk>();
+    else wait_vmcnt<0>();
+    lds_barrier();
+    if (m + 3 < kSteps) request(m + 3);
+    const u32x4* a_src = reinterpret_cast<const u32x4*>(ring + (m % kRing) * kChunkBytes);
+    // Operand reads run kAhead MFMAs ahead of their use (register rotation);
+    // the 8 tiles' hi passes come first, then their lo passes.
+    constexpr int kAhead = 6;
+    bf16x8 a[kAhead];
 #pragma unroll
-  for (int j = 0; j < kVecPerThread; ++j)
-    reinterpret_cast<u32x4*>(lds[0])[tid + j * kFusedWaves * 64] = stage[j];
-  __syncthreads();
-
+    for (int i = 0; i < kAhead; ++i) a[i] = __builtin_bit_cast(bf16x8, a_src[i * 64 + lane]);
 #pragma unroll
-  for (int m = 0; m < 16; ++m) {
-    const int buf = m & 1;
-    if (m + 1 < 16) {
-#pragma unroll
-      for (int j = 0; j < kVecPerThread; ++j)
-        stage[j] = gsrc[(m + 1) * kVecPerChunk + tid + j * kFusedWaves * 64];
+    for (int i = 0; i < 16; ++i) {
+      const bf16x8 cur = a[i % kAhead];
+      if (i + kAhead < 16) a[i % kAhead] = __builtin_bit_cast(bf16x8, a_src[(i + kAhead) * 64 + lane]);
+      acc[i & 7] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur, xb[m], acc[i & 7], 0, 0, 0);
     }
-    const u32x4* a_src = reinterpret_cast<const u32x4*>(lds[buf]);
+    // Keep that pipeline in the schedule: kAhead LDS reads, then each MFMA
+    // followed by the read kAhead positions ahead.
+    __builtin_amdgcn_sched_group_barrier(0x100, kAhead, 0);
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        const bf16x8 a = __builtin_bit_cast(bf16x8, a_src[(p * 8 + t) * 64 + lane]);
-        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, xb[m], acc[t], 0, 0, 0);
-      }
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i + kAhead < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    if (m + 1 < 16) {
-#pragma unroll
-      for (int j = 0; j < kVecPerThread; ++j)
-        reinterpret_cast<u32x4*>(lds[buf ^ 1])[tid + j * kFusedWaves * 64] = stage[j];
-    }
-    __syncthreads();
   }
+  __syncthreads();      // the ring becomes the waves' selection buffers
 
   float v[kPerLane];
 #pragma unroll
@@ -266,7 +431,8 @@ __global__ __launch_bounds__(512) void quant_write_fused_kernel(
 #pragma unroll
     for (int i = 0; i < 16; ++i) v[16 * t + i] = acc[t][i];
   }
-  const QParams p = vector_params(v, side == 0 ? clip_k : clip_v);
+  SelLds& sel = reinterpret_cast<SelLds*>(ring)[wave];
+  const QParams p = vector_params(v, side == 0 ? clip_k : clip_v, sel, lane);
   quantize_store(v, p, live ? slots[tok] : -1, head, side, half, c);
 }
 
@@ -372,9 +538,16 @@ int oscar_quant_write(const void* key_bf16, const void* value_bf16, int64_t num_
               block_size, num_pages * (int64_t)block_size};
   int st = check_cache_args(c);
   if (st != kOk) return st;
+  static bool lds_attr_set = false;
+  if (!lds_attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(quant_write_fused_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kFusedLds) != hipSuccess)
+      return kErrLaunch;
+    lds_attr_set = true;
+  }
   const int64_t per_block = kFusedWaves * kTokPerWave;
   dim3 grid((unsigned)((num_tokens + per_block - 1) / per_block), (unsigned)(num_kv_heads * 2));
-  hipLaunchKernelGGL(quant_write_fused_kernel, grid, dim3(kFusedWaves * 64), 0, stream,
+  hipLaunchKernelGGL(quant_write_fused_kernel, grid, dim3(kFusedWaves * 64), kFusedLds, stream,
                      static_cast<const uint16_t*>(key_bf16), static_cast<const uint16_t*>(value_bf16),
                      num_tokens, token_stride, static_cast<const uint8_t*>(rot_k_operand),
                      static_cast<const uint8_t*>(rot_v_operand), slot_mapping, c,

@@ -151,3 +151,48 @@ def test_fused_rotation_within_tolerance(device, hk):
         mask = torch.ones(pages * bs, dtype=torch.bool)
         mask[valid] = False
         assert not flat[mask].any()
+
+
+def _threshold_cases(seed: int) -> torch.Tensor:
+    """Vectors that stress the clip-threshold search: Gaussian, heavy tails,
+    planted ties at the usual clip ranks, values straddling bucket edges,
+    few distinct values, and magnitudes spread over many octaves."""
+    g = torch.Generator().manual_seed(seed)
+    rows = []
+    for _ in range(16):
+        rows.append(torch.randn(D, generator=g) * 1.4)
+    for _ in range(8):
+        rows.append(torch.empty(D).exponential_(generator=g) * torch.sign(torch.randn(D, generator=g)))
+    for k in (11, 21):
+        x = torch.randn(D, generator=g)
+        top = x.abs().argsort(descending=True)
+        x[top[k - 3:k + 3]] = x[top[k - 1]].abs() * torch.sign(x[top[k - 3:k + 3]])    # 6-way tie at rank k
+        rows.append(x)
+    edge = torch.randn(D, generator=g)
+    a = edge.abs().max()
+    # magnitudes a * 2^(-j/32) sit exactly on the buckets' edges
+    edge[:64] = a * torch.pow(2.0, -torch.arange(64, dtype=torch.float32) / 32) * torch.sign(edge[:64])
+    rows.append(edge)
+    rows.append(torch.randint(-3, 4, (D,), generator=g).float() * 0.5)       # seven distinct values
+    rows.append(torch.exp(torch.randn(D, generator=g) * 3.0) * torch.sign(torch.randn(D, generator=g)))
+    rows.append(torch.cat([torch.full((20,), 50.0), torch.randn(D - 20, generator=g) * 1e-3]))
+    return torch.stack(rows)
+
+
+@pytest.mark.parametrize("idx", [0, 1, 64, 128, 200, 235, 240, 245, 250, 254, 255])
+def test_clip_threshold_search_bit_exact(device, idx):
+    """Every clip rank on adversarial vectors: bytes identical to the sort-based oracle."""
+    k_rot = _threshold_cases(31).unsqueeze(1)
+    v_rot = _threshold_cases(47).unsqueeze(1)
+    N, hk, bs = k_rot.shape[0], 1, 16
+    slots = torch.arange(N, dtype=torch.int64)
+    ratio = (idx + 0.5) / D                      # clip_index(ratio) == idx
+    assert quant.clip_index(ratio, D) == idx
+    caches = [torch.zeros((N + bs - 1) // bs, bs, hk, D, dtype=torch.int8) for _ in range(2)]
+    expect = oracle_store(k_rot, v_rot, caches, slots, ratio, ratio)
+    dev = [c.to(device) for c in caches]
+    quant.quant_write_prerotated(k_rot.to(device), v_rot.to(device), dev[0], dev[1], slots.to(device), idx, idx)
+    torch.cuda.synchronize()
+    for got, want in zip(dev, expect):
+        bad = (got.cpu().view(torch.uint8) != want.view(torch.uint8)).reshape(-1, hk * D)[:N].any(-1)
+        assert not bad.any(), f"rows {bad.nonzero().flatten().tolist()} differ at idx {idx}"
