@@ -89,13 +89,20 @@ __device__ uint32_t select_clip_bits(const float (&v)[kPerLane], int idx, uint32
   uint4* hz = reinterpret_cast<uint4*>(L.hist);
   for (int i = lane; i < 32 * kHistStride / 4; i += 64) hz[i] = uint4{0u, 0u, 0u, 0u};
   wave_sync_lds();
+  // Row t: word 0 absorbs every key below the window, word 1 + j counts key
+  // kl + j (kl = kh - 63), so bucket b from the top (key kh - b) is word 64 - b.
+  // The byte address of key's word is 4 key + (row + 4 - 4 kl) on the 32-bit
+  // LDS address, clamped from below to the absorbing word.
+  typedef __attribute__((address_space(3))) uint32_t lds_u32;
   uint32_t* H = L.hist + t * kHistStride;
   const uint32_t kh = amax_bits >> S;
+  const int32_t row = (int32_t)(uint32_t)(uintptr_t)(lds_u32*)H;
+  const uint32_t base = (uint32_t)(row + 4 - 4 * ((int32_t)kh - (kHistBuckets - 1)));
 #pragma unroll
   for (int i = 0; i < kPerLane; ++i) {
     const uint32_t key = __builtin_amdgcn_ubfe(__float_as_uint(v[i]), S, 31 - S);
-    const uint32_t b = min(kh - key, (uint32_t)kHistBuckets);
-    atomicAdd(&H[b], 1u);
+    const int32_t addr = max((int32_t)((key << 2) + base), row);
+    __atomic_fetch_add((lds_u32*)(uintptr_t)(uint32_t)addr, 1u, __ATOMIC_RELAXED);
   }
   wave_sync_lds();
 
@@ -103,7 +110,7 @@ __device__ uint32_t select_clip_bits(const float (&v)[kPerLane], int idx, uint32
   // 32g .. 32g + 31.
   uint32_t cnt[32];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) cnt[i] = H[32 * g + i];
+  for (int i = 0; i < 32; ++i) cnt[i] = H[kHistBuckets - 32 * g - i];
   uint32_t tot = 0;
 #pragma unroll
   for (int i = 0; i < 32; ++i) tot += cnt[i];
@@ -129,13 +136,17 @@ __device__ uint32_t select_clip_bits(const float (&v)[kPerLane], int idx, uint32
 
   // Gather bucket b*'s values: every value is written at the lane's next free
   // slot, which only advances on a match (capped at the absorbing slot).
+  // The raw bits are stored (sign cleared on reading them back); the match
+  // |x| >> S == keystar is tested on bits << 1, which drops the sign, as one
+  // wrapping subtract and compare.
   uint32_t* mine = L.list + lane * kListStride;
   uint32_t n = 0;
+  const uint32_t lo2 = keystar << (S + 1), w2 = 2u << S;
 #pragma unroll
   for (int i = 0; i < kPerLane; ++i) {
-    const uint32_t u = __float_as_uint(v[i]) & 0x7FFFFFFFu;
+    const uint32_t u = __float_as_uint(v[i]);
     mine[min(n, (uint32_t)kListCap)] = u;
-    n += (u >> S) == keystar ? 1u : 0u;
+    n += ((u << 1) - lo2 < w2) ? 1u : 0u;
   }
   wave_sync_lds();
   const uint32_t n0 = (uint32_t)__shfl((int)n, t, 64), n1 = (uint32_t)__shfl((int)n, t + 32, 64);
@@ -145,8 +156,8 @@ __device__ uint32_t select_clip_bits(const float (&v)[kPerLane], int idx, uint32
   const uint32_t* l1 = L.list + (t + 32) * kListStride;
 #pragma unroll
   for (int i = 0; i < kListCap; ++i) {
-    c[i] = (uint32_t)i < n0 ? l0[i] : 0u;
-    c[kListCap + i] = (uint32_t)i < n1 ? l1[i] : 0u;
+    c[i] = (uint32_t)i < n0 ? l0[i] & 0x7FFFFFFFu : 0u;
+    c[kListCap + i] = (uint32_t)i < n1 ? l1[i] & 0x7FFFFFFFu : 0u;
   }
   // j-th largest of the candidates (j = kk - above >= 1), ties counted.
   uint32_t rem = kk - ab, prev = 0xFFFFFFFFu, res = 0u;
