@@ -283,7 +283,7 @@ def traffic_from_profile(kernel_src: Path):
         return None
 
 
-def cpu_baseline(st, gpu_out, seconds: float):
+def cpu_baseline(st, gpu_out, seconds: float, label: str = "C2"):
     """The oracle's read path on the same (GPU-written) C2 state, on this host.
 
     Also the parity gate of the measured kernel: its output must match the
@@ -317,10 +317,123 @@ def cpu_baseline(st, gpu_out, seconds: float):
     except Exception:
         model = "unknown"
     base = {"value": round(med * 1e6, 1), "unit": "us/layer", "cores": cores, "kind": "port",
-            "sample": f"median of {len(samples)} runs (~{seconds:.0f} s) of the oracle read path on the C2 "
-                      f"layer state (dequant 24579-token INT2 history + FP32 window splice + causal SDPA, "
-                      f"4 queries x 6 heads, fp32); host CPU {model}"}
+            "sample": f"median of {len(samples)} runs (~{seconds:.0f} s) of the oracle read path on the {label} "
+                      f"layer state (dequant {sum(st.seqs) - q.shape[0]}-token INT2 history + FP32 window splice "
+                      f"+ causal SDPA, {q.shape[0]} queries x {q.shape[1]} heads, fp32); host CPU {model}"}
     return base, rel
+
+
+SUITE = {
+    "C3": {"workload": "C3: concurrent MTP decode, 32 requests x 4 query tokens, Hq=6 Hk=1 D=256, histories "
+                       "uniform in [2048, 16384] in 128-token pages drawn from a shared 8192-page pool, FP32 "
+                       "sink=128/recent=256 window (staging 8192), clip 0.96/0.92, 16 distinct layers",
+           "q_len": 4, "pool": 8192, "layers": 16},
+    "C5-decode": {"workload": "C5 decode: 8 requests x 1 query token, 32768-token histories, Hq=6 Hk=1 D=256, "
+                              "pages scattered over a 2056-page pool (2048 history pages + 8 for the step's "
+                              "token), FP32 sink=128/recent=256 window (staging 8192), 16 distinct layers",
+                  "q_len": 1, "pool": 2056, "layers": 16},
+    "C4": {"workload": "C4: prefill continuation, 1 request, 15360-token INT2 history + 9256 new tokens "
+                       "(causal over history + new), Hq=6 Hk=1 D=256, 128-token pages, FP32 window"},
+}
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def suite_histories(name: str):
+    import torch
+
+    if name == "C3":
+        g = torch.Generator().manual_seed(2024)
+        return [int(x) for x in torch.randint(2048, 16385, (32,), generator=g)]
+    return [32768] * 8
+
+
+def bench_prefill(args, dev, seed=71):
+    """C4: the prefill-continuation kernel on the written 15360 + 9256 state."""
+    import torch
+
+    from oscar_amd.kernels import prefill
+
+    hist, new = 15360, 9256
+    st = build_layer(dev, [hist], new, pool=(hist + new + BS - 1) // BS, seed=seed)
+    stage = st.stage()
+    stage3 = None if stage is None else stage[:3]
+
+    def run():
+        return prefill.prefill_continuation(st.q_rot, st.k_rot, st.v_rot, st.caches[0], st.caches[1],
+                                            st.bt[0], hist, st.impl.scale, stage3)
+
+    for _ in range(2):
+        out = run()
+    torch.cuda.synchronize()
+    reps = 10
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        run()
+    e1.record(stream)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / reps
+    visible = new * (hist + 1) + new * (new - 1) // 2
+    flops = 4 * D * HQ * visible
+    return {"us": us, "flops": flops, "tflops": flops / (us * 1e-6) / 1e12, "state": st, "out0": out}
+
+
+def prefill_cpu_baseline(st, gpu_out, hist: int, seconds: float):
+    """The oracle's dense read path for C4 (dequant + splice + chunked causal SDPA), and the parity
+    of the timed kernel against it (bf16 contract: 2e-2 + 2^-8 |oracle| elementwise)."""
+    import torch
+
+    from oracle import attention as oatt
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    q, k, v = st.q_rot.cpu(), st.k_rot.cpu(), st.v_rot.cpu()
+    kc, vc, bt = st.caches[0].cpu(), st.caches[1].cpu(), st.bt.cpu()
+    stage = tuple(t.cpu() for t in st.stage()[:3]) if st.stage() is not None else None
+    samples, want = [], None
+    t_end = time.perf_counter() + seconds
+    while not samples or (time.perf_counter() < t_end and len(samples) < 6):
+        t0 = time.perf_counter()
+        want = oatt.paged_attention_ref(q, k, v, kc, vc, bt, st.qsl, st.seqs, st.impl.scale, stage)
+        samples.append(time.perf_counter() - t0)
+    got = gpu_out.cpu()
+    ok = bool(((got - want).abs() <= 2e-2 + 2.0 ** -8 * want.abs()).all())
+    err = (got - want).abs().max().item()
+    return {"value": round(statistics.median(samples) * 1e3, 1), "unit": "ms/layer", "cores": cores,
+            "kind": "port", "sample": f"median of {len(samples)} runs of the oracle dense read path on the "
+                                      f"C4 state (dequant + window splice + chunked causal SDPA, fp32)"}, ok, err
+
+
+def suite(args, dev):
+    """One JSON line per extra workload: C3 and C5 decode (HBM roofline), C4 prefill (MFMA roofline)."""
+    for name in args.suite.split(","):
+        cfg = SUITE[name]
+        if name == "C4":
+            r = bench_prefill(args, dev)
+            cpu, ok, err = prefill_cpu_baseline(r["state"], r["out0"], 15360, args.cpu_seconds)
+            if not ok:
+                raise SystemExit(f"C4 parity gate failed: max abs err {err:.3e}")
+            line = {"config": name, "workload": cfg["workload"], "value": round(r["us"], 2),
+                    "unit": "us/layer", "arith": "bf16-contract: INT2 dequant to f16, f16 MFMA, f32 softmax",
+                    "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1),
+                                 "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                 "frac": round(r["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4), "flops": r["flops"]},
+                    "parity_max_abs_err": err, "cpu_baseline": cpu}
+        else:
+            hist = suite_histories(name)
+            dec = bench_decode(args, dev, hist, cfg["q_len"], pool=cfg["pool"], layers=cfg["layers"])
+            cpu, rel = cpu_baseline(dec["state"], dec["out0"], args.cpu_seconds, name)
+            if not rel <= 1e-3:
+                raise SystemExit(f"{name} parity gate failed: rel err {rel:.3e}")
+            line = {"config": name, "workload": cfg["workload"], "value": round(dec["us_per_layer"], 3),
+                    "unit": "us/layer", "steps": dec["steps"],
+                    "roofline": {"bound": "hbm", "achieved": round(dec["gbps"], 1), "peak": HBM_PEAK_GBPS,
+                                 "unit": "GB/s", "frac": round(dec["gbps"] / HBM_PEAK_GBPS, 4),
+                                 "bytes_per_layer": dec["bytes"]["total"]},
+                    "history_tokens": sum(hist), "staged_tokens": dec["bytes"]["staged_tokens"],
+                    "parity_rel_err": rel, "cpu_baseline": cpu}
+        print(json.dumps(line), flush=True)
 
 
 def main():
@@ -337,6 +450,9 @@ def main():
     ap.add_argument("--window", type=int, default=1, help="diagnostic: 0 disables the FP32 window")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run a plain device copy of this many MiB first (PMC byte-counter calibration)")
+    ap.add_argument("--suite", default="",
+                    help="comma list of extra workloads (C3, C5-decode, C4): one JSON line each instead "
+                         "of the headline line")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (one TP rank's share "
@@ -347,6 +463,9 @@ def main():
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
     dev = torch.device("cuda:0")
+    if args.suite:
+        suite(args, dev)
+        return
     if args.copy_probe_mib > 0:
         copy_probe(dev, args.copy_probe_mib)
     log("bench: decode C2")

@@ -58,17 +58,21 @@ namespace {
 constexpr int kTile = 32;
 constexpr int kWaves = 4;
 constexpr int kRows = 32;
+constexpr int kStepTok = kWaves * kTile;  // history tokens per step: one tile per wavefront
 constexpr int kMaxFresh = 16;
-constexpr int kVtStride = 9;            // dwords per V code byte-row (32 tokens + pad)
+constexpr int kPRow = 40;               // halves per P' row: 32 token slots + pad (16-byte rows)
+constexpr int kVtRow = 10;              // dwords per V code byte row: 8 groups of 4 tokens + pad
+constexpr int kTRow = 68;               // floats per staged output row: 64 features + pad
+constexpr int kTFloats = kRows * kTRow;
 constexpr int kImgHalfs = 16 * 64 * 8;  // one staged operand image: 16 blocks x 64 lanes x 8
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 4.f;            // log2 headroom before a running max is raised
 constexpr float kLazyVsMax = 4094.f;    // 16 * 4094 < 65504 (fp16 max)
-constexpr int kMaxTilesPerSplit = 256;
-constexpr int kMaxWaveTiles = kMaxTilesPerSplit / kWaves;
+constexpr int kMaxTilesPerSplit = 256;  // 64 steps: one page-register lane per step
 constexpr int kMaxSplits = 1023;        // history splits; the fresh partial makes 1024
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 
 // Work items of one launch travel inside the kernel arguments (no device
 // round trip for the metadata); larger batches are launched in chunks.
@@ -106,19 +110,25 @@ struct DecodeArgs {
   ItemInfo items[kMaxInlineItems];
 };
 
+// One step is 128 history tokens, one 32-token tile per wavefront.  Its
+// exchange buffers are double-buffered across steps.
+struct StepLds {
+  _Float16 p[kWaves][kRows * kPRow];       // P' = p * vs of each tile's INT2 tokens, [row][slot]
+  _Float16 pw[kWaves][kRows * kPRow];      // p / 4 of each tile's window tokens, [row][slot]
+  uint32_t vt[kWaves][64 * kVtRow];        // V code bytes, [byte][group of 4 tokens]
+  float mx[kWaves][kRows];                 // each tile's row maxima
+  uint32_t big[kWaves];                    // the tile holds a V scale above kLazyVsMax
+};
+
 struct MainLds {
-  _Float16 img[kWaves][2][kImgHalfs];             // staged K / V operand images (combine buffers alias)
-  _Float16 q[16 * 2 * kRows * 8];                 // Q^T operand [m][g][row][8]
-  float qsum[kRows];                              // sum of each row's fp16 q
-  uint32_t vt[kWaves][64 * kVtStride];            // V codes [byte][token/4]
-  float ta[kWaves][kTile];                        // score = ta * (q.k') + tb * qsum (+ tm)
+  _Float16 q[16 * 2 * kRows * 8];          // Q^T operand [m][g][row][8]
+  float qsum[kRows];                       // sum of each row's fp16 q
+  float ta[kWaves][kTile];                 // score = ta * acc + tb * qsum + tm (own tile)
   float tb[kWaves][kTile];
-  float tm[kWaves][kTile];                        // 0, or -inf for a token left out of the INT2 pass
-  float tvs[kWaves][kTile];                       // V scale (0: left out)
-  float tvz[kWaves][kTile];                       // V zero
-  float mrow[kWaves][kRows];
-  float lrow[kWaves][kRows];
-  uint32_t defmask[kWaves][kMaxWaveTiles];        // window-token masks of deferred tiles
+  float tm[kWaves][kTile];                 // 0, or -inf for a token left out
+  float tvs[kWaves][kTile];                // V scale of an INT2 token (else 0)
+  float tvz[kWaves][kTile];                // V zero of an INT2 token (else 0)
+  StepLds buf[2];
 };
 
 struct FreshLds {
@@ -127,7 +137,7 @@ struct FreshLds {
 };
 
 constexpr size_t kLdsBytes = sizeof(MainLds) > sizeof(FreshLds) ? sizeof(MainLds) : sizeof(FreshLds);
-static_assert(kLdsBytes <= 160 * 1024, "one workgroup's LDS must fit the CU's 160 KiB");
+static_assert(kLdsBytes <= 80 * 1024, "two workgroups' LDS must fit the CU's 160 KiB");
 
 constexpr int kPartO = kRows * kHeadDim;          // row-major O partial
 constexpr size_t kPartialFloats = kPartO + 2 * kRows;
@@ -163,58 +173,70 @@ __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
-__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
-// Copy one staged operand image (16 KB) into a wave-owned LDS buffer.
-__device__ __forceinline__ void image_to_lds(const _Float16* src, _Float16* dst, int lane) {
-#pragma unroll
-  for (int i = 0; i < 16; ++i)
-    __builtin_amdgcn_global_load_lds(src + (i * 64 + lane) * 8, dst + i * 64 * 8, 16, 0, 0);
+// s_barrier without the memory fence __syncthreads carries: the fence would
+// wait for every outstanding global load, including the next step's, which
+// are meant to stay in flight.  LDS writes are complete at lgkmcnt(0).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);       // lgkmcnt(0); vmcnt and expcnt left at their maxima
+  asm volatile("s_barrier" ::: "memory");
 }
 
-struct TileLoad {
-  u32x4 kc0, kc1;     // this lane's 32 K code bytes
+// One step's loads of one wavefront: its own tile's K codes, meta and V codes,
+// and the owner tags of all 128 tokens of the step (lane l: tokens l, 64 + l).
+struct StepLoad {
+  u32x4 kc0, kc1;     // this lane's 32 K code bytes (token col, half g)
   u32x2 meta;         // K scale, K zero, V scale, V zero (fp16 pairs)
   u32x2 vc[4];        // V code bytes 8*bg .. +7 of tokens 4*tq .. +3
-  int64_t own;        // owner tag of this lane's token seat (-2: no arena)
-  int32_t page;       // -1: tile invalid
-  int32_t prow0;
+  int32_t own0, own1; // owner tags, low 32 bits (meaningful only with an arena)
 };
 
-// Loads of one tile whose page is already known (wave-uniform).  Every lane
-// issues the same loads whatever the tile holds (tokens past the history read
-// an in-bounds row of the page, an invalid tile reads page 0, no arena reads
-// the slot's own bytes), so the compiler can wait for exactly one tile's loads
-// while the next tile's are in flight; results that must not count are
-// neutralised afterwards.
-__device__ __forceinline__ TileLoad load_tile(const DecodeArgs& a, int page, int p0, int prefix, int kvh,
-                                              int lane) {
-  TileLoad L;
-  const bool tile_ok = p0 < prefix && page >= 0;
-  const int pg = tile_ok ? page : 0;
-  L.page = tile_ok ? page : -1;
-  L.prow0 = p0 - (p0 / a.block_size) * a.block_size;
+// Every lane issues the same loads whatever the step holds (tokens past the
+// history read an in-bounds row, an invalid tile reads page 0, no arena reads
+// slot bytes), so the compiler can wait for exactly one step's loads while the
+// next step's are in flight; results that must not count are neutralised
+// where they are used.
+__device__ __forceinline__ StepLoad load_step(const DecodeArgs& a, const int (&pg)[kWaves], int tbase, int prefix,
+                                              int kvh, int w, int lane) {
+  StepLoad L;
   const int t = lane & 31, g = lane >> 5;
   const int tq = lane & 7, bg = lane >> 3;
-  const uint8_t* kbase = a.k_cache + (int64_t)pg * a.k_page + (int64_t)kvh * a.k_head;
-  const uint8_t* vbase = a.v_cache + (int64_t)pg * a.v_page + (int64_t)kvh * a.v_head;
-  const bool tok_ok = tile_ok && p0 + t < prefix;
-  const int trow = tok_ok ? L.prow0 + t : 0;
+  const int p0 = tbase + kTile * w;
+  const int page = pg[w];
+  const bool tile_ok = p0 < prefix && page >= 0;
+  const int pgc = tile_ok ? page : 0;
+  const int prow0 = p0 % a.block_size;
+  const uint8_t* kbase = a.k_cache + (int64_t)pgc * a.k_page + (int64_t)kvh * a.k_head;
+  const uint8_t* vbase = a.v_cache + (int64_t)pgc * a.v_page + (int64_t)kvh * a.v_head;
+  const int trow = (tile_ok && p0 + t < prefix) ? prow0 + t : 0;
   const uint8_t* ks = kbase + (int64_t)trow * a.k_tok;
   L.meta = *reinterpret_cast<const u32x2*>(ks);
   L.kc0 = *reinterpret_cast<const u32x4*>(ks + kKCodeOff + 32 * g);
   L.kc1 = *reinterpret_cast<const u32x4*>(ks + kKCodeOff + 32 * g + 16);
-  const bool arena = a.stage_rows > 0;
-  const int64_t* op = arena ? a.owner + (int64_t)(pg % a.stage_rows) * a.block_size + trow
-                            : reinterpret_cast<const int64_t*>(ks);
-  const int64_t own = *op;
-  L.own = arena ? own : -2;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int tk = 4 * tq + k;
-    const int vrow = (tile_ok && p0 + tk < prefix) ? L.prow0 + tk : 0;
+    const int vrow = (tile_ok && p0 + tk < prefix) ? prow0 + tk : 0;
     L.vc[k] = *reinterpret_cast<const u32x2*>(vbase + (int64_t)vrow * a.v_tok + 8 * bg);
+  }
+  // Owner tags.  The pointers are made opaque so that the loads are always
+  // issued (without an arena the compiler would reuse the meta load instead,
+  // which makes the step's load count path-dependent).
+  typedef __attribute__((address_space(1))) const int32_t global_i32;
+  const bool arena = a.stage_rows > 0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int tk = 64 * h + lane;
+    const int j = tk >> 5;
+    const int pj = j == 0 ? pg[0] : (j == 1 ? pg[1] : (j == 2 ? pg[2] : pg[3]));
+    const int pos = tbase + tk;
+    const bool ok = arena && pj >= 0 && pos < prefix;
+    const int64_t* op = ok ? a.owner + (int64_t)(pj % a.stage_rows) * a.block_size + pos % a.block_size
+                           : reinterpret_cast<const int64_t*>(ks);
+    // Owner tags are pages (< 2^31) or -1: the low word identifies them
+    // (little-endian int64).
+    global_i32* gop = (global_i32*)op;
+    asm volatile("" : "+v"(gop));
+    (h == 0 ? L.own0 : L.own1) = *gop;
   }
   return L;
 }
@@ -239,317 +261,11 @@ __device__ __forceinline__ void k_operands(uint32_t w, uint32_t ones, half8 (&ka
                       magic_pair(w, 8 * aa + 4, ones), magic_pair(w, 8 * aa + 6, ones));
 }
 
-// Online-softmax state of one wavefront: O^T fragments (8 tiles of 32
-// features x 32 rows) and per-row running max / sums.
-struct WaveState {
-  floatx16 acc[8];
-  float m_run, l_run, z_run, ps_run;
-};
-
-// Raise the running max where a tile needs it (rescaling the state only for
-// rows that already hold mass) and return the max the tile's exponents use.
-__device__ __forceinline__ float lazy_max(const floatx16& s, bool eager, WaveState& st) {
-  float mb = -__builtin_inff();
-#pragma unroll
-  for (int r = 0; r < 16; ++r) mb = fmaxf(mb, s[r]);
-  mb = fmaxf(mb, shfl_xor_f32(mb, 32));
-  const bool need = mb > st.m_run + (eager ? 0.f : kLazy);
-  const bool resc = need && st.m_run != -__builtin_inff();
-  if (__ballot(resc)) {
-    const float alpha = resc ? exp2_raw(st.m_run - mb) : 1.f;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) st.acc[t] *= alpha;
-    st.l_run *= alpha;
-    st.z_run *= alpha;
-    st.ps_run *= alpha;
-  }
-  if (need) st.m_run = mb;
-  // exp2(-inf - m) = 0 needs a finite m: rows that have seen no key yet use 0.
-  return st.m_run == -__builtin_inff() ? 0.f : st.m_run;
+// Index of the staged operand image of the tile whose first row is prow0 on
+// `page` (the arena seat row is page % rows).
+__device__ __forceinline__ int64_t image_index(const DecodeArgs& a, int page, int prow0, int kvh) {
+  return ((int64_t)(page % a.stage_rows) * (a.block_size / kTile) + prow0 / kTile) * a.num_kv_heads + kvh;
 }
-
-// Bit mask (token t of the tile -> bit t) of the tile's tokens that the
-// staging arena owns.
-__device__ __forceinline__ uint32_t window_mask(const TileLoad& L, int p0, int prefix, int lane) {
-  const int col = lane & 31;
-  const bool staged = L.page >= 0 && p0 + col < prefix && L.own == (int64_t)L.page;
-  return (uint32_t)__ballot(staged && lane < 32);
-}
-
-__device__ __forceinline__ void issue_images(const DecodeArgs& a, MainLds& S, int page, int prow0, int kvh,
-                                             int w, int lane) {
-  const int64_t img = ((int64_t)(page % a.stage_rows) * (a.block_size / kTile) + prow0 / kTile) *
-                      a.num_kv_heads + kvh;
-  image_to_lds(a.kimg + img * kImgHalfs, S.img[w][0], lane);
-  image_to_lds(a.vimg + img * kImgHalfs, S.img[w][1], lane);
-}
-
-// One history tile from its INT2 codes; tokens in `wmask` (window-owned) and
-// tokens past the history are left out.
-__device__ __forceinline__ void int2_tile(const DecodeArgs& a, MainLds& S, WaveState& st, const TileLoad& L,
-                                          int p0, int prefix, uint32_t wmask, int w, int lane, float qsum,
-                                          uint32_t ones16) {
-  const int g = lane >> 5, col = lane & 31;
-  const int tq = lane & 7, bg = lane >> 3;
-  const int nvalid = L.page >= 0 ? min(kTile, prefix - p0) : 0;
-  const bool used = col < nvalid && !((wmask >> col) & 1u);
-  const bool masked = wmask != 0 || nvalid < kTile;      // wave-uniform
-
-  // ---- V codes -> LDS [byte][token], per-token score/V parameters ----
-  float vsc = 0.f;
-  {
-    uint32_t o0[4], o1[4];
-    transpose4(L.vc[0][0], L.vc[1][0], L.vc[2][0], L.vc[3][0], o0);
-    transpose4(L.vc[0][1], L.vc[1][1], L.vc[2][1], L.vc[3][1], o1);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      S.vt[w][(8 * bg + k) * kVtStride + tq] = o0[k];
-      S.vt[w][(8 * bg + 4 + k) * kVtStride + tq] = o1[k];
-    }
-    if (g == 0) {
-      float av = 0.f, bv = 0.f, vzv = 0.f, tmv = -__builtin_inff();
-      if (used) {
-        const float ks = f16_bits_to_f32(L.meta[0]);
-        const float kz = f16_bits_to_f32(L.meta[0] >> 16);
-        av = 4.f * ks * a.scale_log2;
-        bv = (kz - 4.f * ks) * a.scale_log2;
-        vsc = f16_bits_to_f32(L.meta[1]);
-        vzv = f16_bits_to_f32(L.meta[1] >> 16);
-        tmv = 0.f;
-      }
-      S.ta[w][col] = av;
-      S.tb[w][col] = bv;
-      S.tm[w][col] = tmv;
-      S.tvs[w][col] = vsc;
-      S.tvz[w][col] = vzv;
-    }
-  }
-  const bool vs_big = __ballot(vsc > kLazyVsMax) != 0;
-  wave_sync_lds();
-
-  // ---- S^T = K' Q^T (all Q^T operand reads in flight together; two
-  // accumulator chains) ----
-  half8 qb[16];
-#pragma unroll
-  for (int m = 0; m < 16; ++m) qb[m] = *reinterpret_cast<const half8*>(&S.q[((m * 2 + g) * kRows + col) * 8]);
-  const uint32_t kw[8] = {L.kc0[0], L.kc0[1], L.kc0[2], L.kc0[3], L.kc1[0], L.kc1[1], L.kc1[2], L.kc1[3]};
-  floatx16 s0 = floatx16{}, s1 = floatx16{};
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    half8 ka[2];
-    k_operands(kw[j], ones16, ka);
-    if (j & 1) {
-      s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[0], qb[2 * j], s1, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[1], qb[2 * j + 1], s1, 0, 0, 0);
-    } else {
-      s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[0], qb[2 * j], s0, 0, 0, 0);
-      s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[1], qb[2 * j + 1], s0, 0, 0, 0);
-    }
-  }
-  floatx16 s = s0 + s1;
-
-  // ---- scores and lazy online softmax (lane: row `col`, tokens 8*(r/4) + 4*g + r%4) ----
-#pragma unroll
-  for (int jj = 0; jj < 4; ++jj) {
-    const floatx4 av = *reinterpret_cast<const floatx4*>(&S.ta[w][8 * jj + 4 * g]);
-    const floatx4 bv = *reinterpret_cast<const floatx4*>(&S.tb[w][8 * jj + 4 * g]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) s[4 * jj + i] = fmaf(av[i], s[4 * jj + i], bv[i] * qsum);
-  }
-  if (masked) {
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const floatx4 tmv = *reinterpret_cast<const floatx4*>(&S.tm[w][8 * jj + 4 * g]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s[4 * jj + i] += tmv[i];
-    }
-  }
-  const float m_use = lazy_max(s, vs_big, st);
-  half8 pb[2];
-  float psum = 0.f, zsum = 0.f;
-#pragma unroll
-  for (int jj = 0; jj < 4; ++jj) {
-    const floatx4 vsv = *reinterpret_cast<const floatx4*>(&S.tvs[w][8 * jj + 4 * g]);
-    const floatx4 vze = *reinterpret_cast<const floatx4*>(&S.tvz[w][8 * jj + 4 * g]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 4 * jj + i;
-      const float p = exp2_raw(s[r] - m_use);
-      psum += p;
-      zsum = fmaf(p, vze[i], zsum);
-      s[r] = p * vsv[i];          // P' (scale folded)
-    }
-  }
-  const half2v ones{(_Float16)1.f, (_Float16)1.f};
-  // slot u <-> tokens (t0, t2, t1, t3, t4, t6, t5, t7) of each 8-token group
-#pragma unroll
-  for (int mm = 0; mm < 2; ++mm) {
-    const int r0 = 8 * mm;
-    pb[mm] = half8{(_Float16)s[r0 + 0], (_Float16)s[r0 + 2], (_Float16)s[r0 + 1], (_Float16)s[r0 + 3],
-                   (_Float16)s[r0 + 4], (_Float16)s[r0 + 6], (_Float16)s[r0 + 5], (_Float16)s[r0 + 7]};
-    float pss = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      pss = __builtin_amdgcn_fdot2(half2v{pb[mm][2 * e], pb[mm][2 * e + 1]}, ones, pss, false);
-    st.ps_run += pss;
-  }
-  st.l_run += psum;
-  st.z_run += zsum;
-
-  // ---- O^T += V'^T P'^T ----
-#pragma unroll
-  for (int mm = 0; mm < 2; ++mm) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t* vrow = &S.vt[w][(32 * h + col) * kVtStride];
-      const uint32_t d0 = vrow[4 * mm + g];
-      const uint32_t d1 = vrow[4 * mm + 2 + g];
-#pragma unroll
-      for (int sp = 0; sp < 4; ++sp) {
-        const half8 va = as_half8(magic_pair(d0, 2 * sp, ones16), magic_pair(d0, 2 * sp + 8, ones16),
-                                  magic_pair(d1, 2 * sp, ones16), magic_pair(d1, 2 * sp + 8, ones16));
-        st.acc[4 * h + sp] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[mm], st.acc[4 * h + sp], 0, 0, 0);
-      }
-    }
-  }
-  wave_sync_lds();
-}
-
-// The window-owned tokens `wmask` of a tile whose operand images are in the
-// wave's LDS buffers: exact fp16 K / V values, probabilities into the PV pass
-// as p / 4 (the state's O^T is scaled by 4 at the end).
-__device__ __forceinline__ void window_tile(const DecodeArgs& a, MainLds& S, WaveState& st, uint32_t wmask,
-                                            int w, int lane) {
-  const int g = lane >> 5, col = lane & 31;
-  const _Float16* kb = S.img[w][0];
-  const _Float16* vb = S.img[w][1];
-  floatx16 s0 = floatx16{}, s1 = floatx16{};
-#pragma unroll
-  for (int m0 = 0; m0 < 16; m0 += 8) {
-    half8 ka[8], qb[8];
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      ka[m] = *reinterpret_cast<const half8*>(kb + ((m0 + m) * 64 + lane) * 8);
-      qb[m] = *reinterpret_cast<const half8*>(&S.q[(((m0 + m) * 2 + g) * kRows + col) * 8]);
-    }
-#pragma unroll
-    for (int m = 0; m < 8; m += 2) {
-      s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[m], qb[m], s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[m + 1], qb[m + 1], s1, 0, 0, 0);
-    }
-  }
-  floatx16 s = s0 + s1;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int tok = 8 * (r >> 2) + 4 * g + (r & 3);
-    s[r] = ((wmask >> tok) & 1u) ? s[r] * a.scale_log2 : -__builtin_inff();
-  }
-  const float m_use = lazy_max(s, false, st);
-  float q4[16];
-  float psum = 0.f;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const float p = exp2_raw(s[r] - m_use);
-    psum += p;
-    q4[r] = 0.25f * p;
-  }
-  st.l_run += psum;
-#pragma unroll
-  for (int mm = 0; mm < 2; ++mm) {
-    const float* e = q4 + 8 * mm;
-    const half8 ps = half8{(_Float16)e[0], (_Float16)e[2], (_Float16)e[1], (_Float16)e[3],
-                           (_Float16)e[4], (_Float16)e[6], (_Float16)e[5], (_Float16)e[7]};
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-#pragma unroll
-      for (int sp = 0; sp < 4; ++sp) {
-        const half8 va = *reinterpret_cast<const half8*>(vb + ((((h * 4 + sp) * 2 + mm) * 64) + lane) * 8);
-        st.acc[4 * h + sp] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ps, st.acc[4 * h + sp], 0, 0, 0);
-      }
-    }
-  }
-}
-
-// ---- cross-wave reduce-scatter of the O^T fragments ----
-// Round 1 pairs waves w and w ^ 2: wave w keeps tiles 4H .. 4H + 3 (H = w / 2)
-// and sends the other four.  Round 2 pairs w and w ^ 1: wave w keeps the
-// fragment registers 8J .. 8J + 7 (J = w % 2) of its tiles and sends the rest.
-constexpr int kR1Floats = 4 * 4 * 64 * 4;   // per wave: 4 tiles x 4 register quads x 64 lanes x 4
-constexpr int kR2Floats = 4 * 2 * 64 * 4;
-
-// Fragments enter the exchange already finished: x -> x * f4 + off (the
-// wave's share of the common max, the 1 + c/4 code offset and the V zeros).
-template <int W>
-__device__ __forceinline__ void rs_send1(const floatx16 (&acc)[8], float f4, float off, float* cb, int lane) {
-  constexpr int Hs = 1 - (W >> 1);
-  float* dst = cb + W * kR1Floats;
-#pragma unroll
-  for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-    for (int jq = 0; jq < 4; ++jq) {
-      const floatx16& x = acc[4 * Hs + tt];
-      *reinterpret_cast<floatx4*>(dst + ((tt * 4 + jq) * 64 + lane) * 4) =
-          floatx4{fmaf(x[4 * jq], f4, off), fmaf(x[4 * jq + 1], f4, off), fmaf(x[4 * jq + 2], f4, off),
-                  fmaf(x[4 * jq + 3], f4, off)};
-    }
-}
-
-template <int W>
-__device__ __forceinline__ void rs_recv1_send2(floatx16 (&acc)[8], float f4, float off, float* cb, int lane) {
-  constexpr int H = W >> 1, J = W & 1, Js = 1 - J;
-  const float* src = cb + (W ^ 2) * kR1Floats;
-#pragma unroll
-  for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-    for (int jq = 0; jq < 4; ++jq) {
-      const floatx4 v = *reinterpret_cast<const floatx4*>(src + ((tt * 4 + jq) * 64 + lane) * 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        acc[4 * H + tt][4 * jq + i] = fmaf(acc[4 * H + tt][4 * jq + i], f4, off) + v[i];
-    }
-  float* dst = cb + 4 * kR1Floats + W * kR2Floats;
-#pragma unroll
-  for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const int r0 = 4 * (2 * Js + jj);
-      *reinterpret_cast<floatx4*>(dst + ((tt * 2 + jj) * 64 + lane) * 4) =
-          floatx4{acc[4 * H + tt][r0], acc[4 * H + tt][r0 + 1], acc[4 * H + tt][r0 + 2], acc[4 * H + tt][r0 + 3]};
-    }
-}
-
-// Final round: add the partner's copy of the kept registers and stage this
-// wave's 64 features of every row, [row][64 + 4 pad] fp32, in LDS (register
-// 4jq + i of tile 4H + sp is local feature 32(jq - 2J) + 16g + 4i + sp).
-constexpr int kTRow = 68;
-constexpr int kTFloats = kRows * kTRow;
-
-template <int W>
-__device__ __forceinline__ void rs_recv2_stage(floatx16 (&acc)[8], const float* cb, float* tb, int lane) {
-  constexpr int H = W >> 1, J = W & 1;
-  const float* src = cb + 4 * kR1Floats + (W ^ 1) * kR2Floats;
-  const int g = lane >> 5, col = lane & 31;
-#pragma unroll
-  for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const floatx4 v = *reinterpret_cast<const floatx4*>(src + ((tt * 2 + jj) * 64 + lane) * 4);
-      const int r0 = 4 * (2 * J + jj);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[4 * H + tt][r0 + i] += v[i];
-    }
-  float* row = tb + W * kTFloats + col * kTRow + 16 * g;
-#pragma unroll
-  for (int jj = 0; jj < 2; ++jj) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 4 * (2 * J + jj) + i;
-      *reinterpret_cast<floatx4*>(row + 32 * jj + 4 * i) =
-          floatx4{acc[4 * H][r], acc[4 * H + 1][r], acc[4 * H + 2][r], acc[4 * H + 3][r]};
-    }
-  }
-}
-
 // The step's own new tokens of one item, exact fp32: row (token j, head h)
 // against new keys 0 .. j, written as a partial like a history split's.
 __device__ void fresh_partial(const DecodeArgs& a, const ItemInfo& it, int item, int rt, FreshLds& F) {
@@ -640,7 +356,19 @@ __device__ void fresh_partial(const DecodeArgs& a, const ItemInfo& it, int item,
   }
 }
 
-__global__ __launch_bounds__(256) void paged_decode_split_kernel(DecodeArgs a) {
+__device__ __forceinline__ uint32_t pair_lo(uint32_t d, uint32_t ls, uint32_t ones) {
+  return ((d << ls) & 0x03000300u) | ones;     // code of bytes 0 and 2 -> fp16 pair 1 + c/4
+}
+__device__ __forceinline__ uint32_t pair_hi(uint32_t d, uint32_t rs, uint32_t ones) {
+  return ((d >> rs) & 0x03000300u) | ones;     // code of bytes 1 and 3
+}
+
+template <typename T>
+__device__ __forceinline__ T pick4(T v0, T v1, T v2, T v3, int i) {
+  return i == 0 ? v0 : (i == 1 ? v1 : (i == 2 ? v2 : v3));
+}
+
+__global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
   const int split = blockIdx.x;
   const int item = blockIdx.y;
@@ -653,24 +381,32 @@ __global__ __launch_bounds__(256) void paged_decode_split_kernel(DecodeArgs a) {
     return;
   }
   const int prefix = it.prefix;
-  const int tiles = (prefix + kTile - 1) / kTile;
-  if (split >= tiles) return;
+  const int steps = (prefix + kStepTok - 1) / kStepTok;
+  if (split >= steps) return;
   MainLds& S = *reinterpret_cast<MainLds*>(smem_raw);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5;
   const int col = lane & 31;
   const int kvh = it.kvh;
   const int nsplit = a.max_splits;
-  const int tstep = nsplit * kWaves;
-  const int first = split + nsplit * w;
-  const int ntw = first < tiles ? (tiles - 1 - first) / tstep + 1 : 0;
+  const int nst = (steps - 1 - split) / nsplit + 1;     // steps split + nsplit k, k < nst (<= 64)
+  const bool arena = a.stage_rows > 0;
 
-  // ---- requests before any wait: this thread's query features and the
-  // wave's pages (lane k: page of the wave's k-th tile), then the first two
-  // tiles' loads, which are in flight while Q is converted ----
+  // ---- requests before any wait: the pages of the workgroup's tiles (lane k
+  // of pgv[j]: tile j of step k), the query features, then the first step ----
+  int pgv[kWaves];
+#pragma unroll
+  for (int j = 0; j < kWaves; ++j) {
+    pgv[j] = -1;
+    const int64_t tok0 = (int64_t)(split + nsplit * lane) * kStepTok + kTile * j;
+    if (lane < nst && tok0 < prefix) {
+      const int64_t pidx = tok0 / a.block_size;
+      if (pidx < a.bt_cols) pgv[j] = a.block_table[(int64_t)it.req * a.bt_stride + pidx];
+    }
+  }
   const int r8 = tid >> 3, c8 = tid & 7;
   floatx4 x[8];
   {
@@ -682,17 +418,26 @@ __global__ __launch_bounds__(256) void paged_decode_split_kernel(DecodeArgs a) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) x[k] = src[k];
   }
-  int my_page = -1;
-  if (lane < ntw) {
-    const int pidx = (first + tstep * lane) * kTile / a.block_size;
-    if (pidx < a.bt_cols) my_page = a.block_table[(int64_t)it.req * a.bt_stride + pidx];
+  auto step_pages = [&](int k, int (&pg)[kWaves]) {
+#pragma unroll
+    for (int j = 0; j < kWaves; ++j) {
+      const int p = __builtin_amdgcn_readlane(pgv[j], k);
+      pg[j] = (p >= 0 && p < a.num_pages) ? p : -1;
+    }
+  };
+  int pg[kWaves];
+  step_pages(0, pg);
+  StepLoad cur = load_step(a, pg, split * kStepTok, prefix, kvh, w, lane);
+  // Touch the pages of this wave's later tiles in both caches now (lane k:
+  // step k), so that their address translations overlap the first step
+  // instead of each step's own loads.
+  uint32_t touched;
+  {
+    const int pk = pick4(pgv[0], pgv[1], pgv[2], pgv[3], w);
+    const int64_t pgk = (lane < nst && pk >= 0 && pk < a.num_pages) ? pk : 0;
+    touched = *reinterpret_cast<const uint32_t*>(a.k_cache + pgk * a.k_page) ^
+              *reinterpret_cast<const uint32_t*>(a.v_cache + pgk * a.v_page);
   }
-  if (my_page >= a.num_pages) my_page = -1;
-  // @probe:1
-  TileLoad A = load_tile(a, ntw > 0 ? __builtin_amdgcn_readlane(my_page, 0) : -1, first * kTile, prefix, kvh,
-                         lane);
-  TileLoad B = load_tile(a, ntw > 1 ? __builtin_amdgcn_readlane(my_page, 1) : -1, (first + tstep) * kTile,
-                         prefix, kvh, lane);
 
   // ---- Q^T operand into LDS (permuted K dimension, fp16) and row sums ----
   // Thread: row r8, features 32 * c8 .. +31, which are exactly the four
@@ -721,125 +466,285 @@ __global__ __launch_bounds__(256) void paged_decode_split_kernel(DecodeArgs a) {
     qs += shfl_xor_f32(qs, 4);
     if (c8 == 0) S.qsum[r8] = (rt * kRows + r8 < rows) ? qs : 0.f;
   }
-  __syncthreads();
-  // @probe:2
+  lds_barrier();
 
-  WaveState st;
-#pragma unroll
-  for (int t = 0; t < 8; ++t) st.acc[t] = floatx16{};
-  st.m_run = -__builtin_inff();
-  st.l_run = st.z_run = st.ps_run = 0.f;
+  floatx16 acc[2] = {floatx16{}, floatx16{}};   // O^T of features 64w .. 64w + 63 (2 blocks of 32)
+  float m_run = -__builtin_inff();
+  float l_run = 0.f, z_run = 0.f, ps_run = 0.f;  // this lane's share of its row's sums (own tiles)
   const float qsum = S.qsum[col];
   const uint32_t ones16 = magic_ones();
-  int pend = -1;                 // first tile with window tokens (images in flight)
-  uint32_t pend_mask = 0;
-  uint64_t defer = 0;            // later tiles with window tokens
+  // PV operand lane constants: block b, row m = col is code sp = 2b + (m & 1)
+  // of V code byte 16w + (m >> 1).
+  const int vrow = 16 * w + (col >> 1);
+  const uint32_t e2 = 2u * (uint32_t)(col & 1);
+  const uint32_t ls0 = 8u - e2, rs0 = e2, ls1 = 4u - e2, rs1 = 4u + e2;
 
-  // Window tokens of a tile: the first such tile's images are requested at
-  // once, later ones are deferred.  Both prologue tiles are checked before
-  // any compute so that their images are in flight early.
-  auto note_window = [&](const TileLoad& L, int k, uint32_t wm) {
-    if (wm == 0) return;
-    if (pend < 0) {
-      pend = k;
-      pend_mask = wm;
-      issue_images(a, S, L.page, L.prow0, kvh, w, lane);
-    } else {
-      defer |= 1ull << k;
-      if (lane == 0) S.defmask[w][k] = wm;
+  auto run_step = [&](const StepLoad& L, int k, const int (&pgs)[kWaves]) {
+    const int tbase = (split + nsplit * k) * kStepTok;
+    StepLds& B = S.buf[k & 1];
+    // window-owned tokens of the step's four tiles (bit t of wmj: token t of tile j)
+    uint32_t wm0 = 0u, wm1 = 0u, wm2 = 0u, wm3 = 0u;
+    if (arena) {
+      const int pa = g == 0 ? pgs[0] : pgs[1];
+      const int pb = g == 0 ? pgs[2] : pgs[3];
+      const bool s0 = pa >= 0 && tbase + lane < prefix && L.own0 == pa;
+      const bool s1 = pb >= 0 && tbase + 64 + lane < prefix && L.own1 == pb;
+      const uint64_t b0 = __ballot(s0), b1 = __ballot(s1);
+      wm0 = (uint32_t)b0;
+      wm1 = (uint32_t)(b0 >> 32);
+      wm2 = (uint32_t)b1;
+      wm3 = (uint32_t)(b1 >> 32);
     }
-  };
-  // A tile whose every history token is window-owned skips the INT2 pass.
-  auto all_window = [&](int p0, uint32_t wm) {
-    const int nvalid = min(kTile, prefix - p0);
-    return wm != 0 && wm == (nvalid >= kTile ? 0xFFFFFFFFu : ((1u << nvalid) - 1u));
-  };
-  uint32_t wmA = ntw > 0 ? window_mask(A, first * kTile, prefix, lane) : 0u;
-  uint32_t wmB = ntw > 1 ? window_mask(B, (first + tstep) * kTile, prefix, lane) : 0u;
-  note_window(A, 0, wmA);
-  note_window(B, 1, wmB);
-#pragma unroll 1
-  for (int k = 0; k < ntw; k += 2) {
+    const uint32_t wmw = pick4(wm0, wm1, wm2, wm3, w);
+    const int pgw = pick4(pgs[0], pgs[1], pgs[2], pgs[3], w);
+    const int p0 = tbase + kTile * w;
+    const int nvalid = pgw >= 0 ? min(kTile, max(prefix - p0, 0)) : 0;
+
+    // ---- own tile: token parameters and byte-transposed V codes ----
+    bool big;
     {
-      const int p0 = (first + tstep * k) * kTile;
-      if (k > 0) {
-        wmA = window_mask(A, p0, prefix, lane);
-        note_window(A, k, wmA);
+      const bool win = (wmw >> col) & 1u;
+      const bool used = col < nvalid && !win;
+      const float ksc = f16_bits_to_f32(L.meta[0]);
+      const float kz = f16_bits_to_f32(L.meta[0] >> 16);
+      const float vsc = f16_bits_to_f32(L.meta[1]);
+      const float vz = f16_bits_to_f32(L.meta[1] >> 16);
+      if (g == 0) {
+        S.ta[w][col] = used ? 4.f * ksc * a.scale_log2 : (win ? a.scale_log2 : 0.f);
+        S.tb[w][col] = used ? (kz - 4.f * ksc) * a.scale_log2 : 0.f;
+        S.tm[w][col] = (used || win) ? 0.f : -__builtin_inff();
+        S.tvs[w][col] = used ? vsc : 0.f;
+        S.tvz[w][col] = used ? vz : 0.f;
       }
-      if (!all_window(p0, wmA)) int2_tile(a, S, st, A, p0, prefix, wmA, w, lane, qsum, ones16);
-      if (k + 2 < ntw)
-        A = load_tile(a, __builtin_amdgcn_readlane(my_page, k + 2), p0 + 2 * tstep * kTile, prefix, kvh, lane);
-    }
-    if (k + 1 < ntw) {
-      const int p0 = (first + tstep * (k + 1)) * kTile;
-      if (k > 0) {
-        wmB = window_mask(B, p0, prefix, lane);
-        note_window(B, k + 1, wmB);
-      }
-      if (!all_window(p0, wmB)) int2_tile(a, S, st, B, p0, prefix, wmB, w, lane, qsum, ones16);
-      if (k + 3 < ntw)
-        B = load_tile(a, __builtin_amdgcn_readlane(my_page, k + 3), p0 + 2 * tstep * kTile, prefix, kvh, lane);
-    }
-  }
-  // @probe:3
-
-  // ---- window tokens from their operand images ----
-  if (pend >= 0) {
-    wait_vmem();
-    wave_sync_lds();
-    window_tile(a, S, st, pend_mask, w, lane);
-#pragma unroll 1
-    while (defer) {
-      const int k = __builtin_ctzll(defer);
-      defer &= defer - 1;
-      const int p0 = (first + tstep * k) * kTile;
-      wave_sync_lds();
-      issue_images(a, S, __builtin_amdgcn_readlane(my_page, k), p0 % a.block_size, kvh, w, lane);
-      wait_vmem();
-      wave_sync_lds();
-      window_tile(a, S, st, S.defmask[w][k], w, lane);
-    }
-  }
-  // @probe:4
-
-  // ---- combine the 4 wavefronts: common max, then reduce-scatter in LDS ----
-  const float l_tot = st.l_run + shfl_xor_f32(st.l_run, 32);
-  const float z_tot = st.z_run + shfl_xor_f32(st.z_run, 32);
-  const float ps_tot = st.ps_run + shfl_xor_f32(st.ps_run, 32);
-  if (g == 0) {
-    S.mrow[w][col] = st.m_run;
-    S.lrow[w][col] = l_tot;
-  }
-  __syncthreads();
-  float mx = -__builtin_inff();
+      big = __ballot(used && vsc > kLazyVsMax) != 0;
+      const int tq = lane & 7, bg = lane >> 3;
+      uint32_t o0[4], o1[4];
+      transpose4(L.vc[0][0], L.vc[1][0], L.vc[2][0], L.vc[3][0], o0);
+      transpose4(L.vc[0][1], L.vc[1][1], L.vc[2][1], L.vc[3][1], o1);
 #pragma unroll
-  for (int k = 0; k < kWaves; ++k) mx = fmaxf(mx, S.mrow[k][col]);
-  const float fw = (st.m_run == -__builtin_inff()) ? 0.f : exp2f(st.m_run - mx);
-  const float f4 = 4.f * fw;
-  const float off = (z_tot - 4.f * ps_tot) * fw;
-  float* cb = reinterpret_cast<float*>(&S.img[0][0][0]);
-  switch (w) {
-    case 0: rs_send1<0>(st.acc, f4, off, cb, lane); break;
-    case 1: rs_send1<1>(st.acc, f4, off, cb, lane); break;
-    case 2: rs_send1<2>(st.acc, f4, off, cb, lane); break;
-    default: rs_send1<3>(st.acc, f4, off, cb, lane); break;
+      for (int kk = 0; kk < 4; ++kk) {
+        B.vt[w][(8 * bg + kk) * kVtRow + tq] = o0[kk];
+        B.vt[w][(8 * bg + 4 + kk) * kVtRow + tq] = o1[kk];
+      }
+    }
+    wave_sync_lds();
+
+    // ---- S^T = K Q^T of the own tile (window tokens from their image) ----
+    floatx16 s;
+    {
+      // Q^T operands are read from LDS one k-step pair ahead of their use.
+      const half8* qsrc = reinterpret_cast<const half8*>(&S.q[(g * kRows + col) * 8]);   // + m * 2 * kRows
+      const uint32_t kw[8] = {L.kc0[0], L.kc0[1], L.kc0[2], L.kc0[3], L.kc1[0], L.kc1[1], L.kc1[2], L.kc1[3]};
+      // One accumulator chain: the other workgroup on the SIMD covers the
+      // MFMA latency.
+      s = floatx16{};
+      half8 qa = qsrc[0], qb = qsrc[2 * kRows];
+      auto qk_pair = [&](int j, const half8& k0, const half8& k1) {
+        half8 na = qa, nb = qb;
+        if (j < 7) {
+          na = qsrc[(2 * j + 2) * 2 * kRows];
+          nb = qsrc[(2 * j + 3) * 2 * kRows];
+        }
+        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qa, s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qb, s, 0, 0, 0);
+        qa = na;
+        qb = nb;
+      };
+      if (wmw == 0u) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          half8 ka[2];
+          k_operands(kw[j], ones16, ka);
+          qk_pair(j, ka[0], ka[1]);
+        }
+      } else {
+        const u32x4* img = reinterpret_cast<const u32x4*>(
+            a.kimg + image_index(a, pgw, p0 % a.block_size, kvh) * kImgHalfs);
+        u32x4 im[16];
+#pragma unroll
+        for (int m = 0; m < 16; ++m) im[m] = img[m * 64 + lane];
+        const bool wl = (wmw >> col) & 1u;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          half8 ka[2];
+          k_operands(kw[j], ones16, ka);
+#pragma unroll
+          for (int aa = 0; aa < 2; ++aa)
+            ka[aa] = wl ? __builtin_bit_cast(half8, im[2 * j + aa]) : ka[aa];
+          qk_pair(j, ka[0], ka[1]);
+        }
+      }
+    }
+    // The window tiles' V image blocks of this wave's features are requested
+    // here, a phase before the PV pass uses them.
+    const bool anywin = (wm0 | wm1 | wm2 | wm3) != 0u;
+    half8 vim[kWaves][2][2];
+    if (anywin) {
+#pragma unroll
+      for (int j = 0; j < kWaves; ++j) {
+        const uint32_t wmj = j == 0 ? wm0 : (j == 1 ? wm1 : (j == 2 ? wm2 : wm3));
+        if (wmj != 0u) {
+          const half8* vimg = reinterpret_cast<const half8*>(
+              a.vimg + image_index(a, pgs[j], (tbase + kTile * j) % a.block_size, kvh) * kImgHalfs);
+#pragma unroll
+          for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) vim[j][b][s2] = vimg[((w * 2 + b) * 2 + s2) * 64 + lane];
+        }
+      }
+    }
+    // scores (lane: row col, tokens 8 (r / 4) + 4g + r % 4) and the tile's row max
+    float mb = -__builtin_inff();
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const floatx4 av = *reinterpret_cast<const floatx4*>(&S.ta[w][8 * jj + 4 * g]);
+      const floatx4 bv = *reinterpret_cast<const floatx4*>(&S.tb[w][8 * jj + 4 * g]);
+      const floatx4 tmv = *reinterpret_cast<const floatx4*>(&S.tm[w][8 * jj + 4 * g]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s[4 * jj + i] = fmaf(av[i], s[4 * jj + i], bv[i] * qsum) + tmv[i];
+        mb = fmaxf(mb, s[4 * jj + i]);
+      }
+    }
+    mb = fmaxf(mb, shfl_xor_f32(mb, 32));
+    if (g == 0) B.mx[w][col] = mb;
+    if (lane == 0) B.big[w] = big ? 1u : 0u;
+    lds_barrier();
+
+    // ---- common max of the step (same decision in every wave), P' of the own tile ----
+    {
+      const float M = fmaxf(fmaxf(B.mx[0][col], B.mx[1][col]), fmaxf(B.mx[2][col], B.mx[3][col]));
+      const bool eager = (B.big[0] | B.big[1] | B.big[2] | B.big[3]) != 0u;
+      const bool need = M > m_run + (eager ? 0.f : kLazy);
+      const bool resc = need && m_run != -__builtin_inff();
+      if (__ballot(resc)) {
+        const float alpha = resc ? exp2_raw(m_run - M) : 1.f;
+        acc[0] *= alpha;
+        acc[1] *= alpha;
+        l_run *= alpha;
+        z_run *= alpha;
+        ps_run *= alpha;
+      }
+      if (need) m_run = M;
+    }
+    {
+      // exp2(-inf - m) = 0 needs a finite m: rows that have seen no key yet use 0.
+      const float m_use = m_run == -__builtin_inff() ? 0.f : m_run;
+      float psum = 0.f, zsum = 0.f, pss = 0.f;
+      const half2v ones{(_Float16)1.f, (_Float16)1.f};
+      _Float16* prow = &B.p[w][col * kPRow + 4 * g];
+      _Float16* pwrow = &B.pw[w][col * kPRow + 4 * g];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const floatx4 vsv = *reinterpret_cast<const floatx4*>(&S.tvs[w][8 * jj + 4 * g]);
+        const floatx4 vze = *reinterpret_cast<const floatx4*>(&S.tvz[w][8 * jj + 4 * g]);
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[i] = exp2_raw(s[4 * jj + i] - m_use);
+          psum += p[i];
+          zsum = fmaf(p[i], vze[i], zsum);
+        }
+        // slots 8jj + 4g + {0, 1, 2, 3} hold tokens 8jj + 4g + {0, 2, 1, 3}
+        const half4 h = half4{(_Float16)(p[0] * vsv[0]), (_Float16)(p[2] * vsv[2]), (_Float16)(p[1] * vsv[1]),
+                              (_Float16)(p[3] * vsv[3])};
+        *reinterpret_cast<half4*>(prow + 8 * jj) = h;
+        pss = __builtin_amdgcn_fdot2(half2v{h[0], h[1]}, ones, pss, false);
+        pss = __builtin_amdgcn_fdot2(half2v{h[2], h[3]}, ones, pss, false);
+        if (wmw != 0u) {
+          const uint32_t wb = wmw >> (8 * jj + 4 * g);
+          const half4 hw = half4{(wb & 1u) ? (_Float16)(0.25f * p[0]) : (_Float16)0.f,
+                                 (wb & 4u) ? (_Float16)(0.25f * p[2]) : (_Float16)0.f,
+                                 (wb & 2u) ? (_Float16)(0.25f * p[1]) : (_Float16)0.f,
+                                 (wb & 8u) ? (_Float16)(0.25f * p[3]) : (_Float16)0.f};
+          *reinterpret_cast<half4*>(pwrow + 8 * jj) = hw;
+        }
+      }
+      l_run += psum;
+      z_run += zsum;
+      ps_run += pss;
+    }
+    lds_barrier();
+
+    // ---- O^T (features 64w .. 64w + 63) += V^T P'^T over the step's tiles ----
+#pragma unroll
+    for (int j = 0; j < kWaves; ++j) {
+      if (pgs[j] < 0 || tbase + kTile * j >= prefix) continue;
+      const uint32_t* vr = &B.vt[j][vrow * kVtRow];
+      const _Float16* pr = &B.p[j][col * kPRow + 8 * g];
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const uint32_t d0 = vr[4 * s2 + 2 * g], d1 = vr[4 * s2 + 2 * g + 1];
+        const half8 pop = *reinterpret_cast<const half8*>(pr + 16 * s2);
+        const half8 v0 = as_half8(pair_lo(d0, ls0, ones16), pair_hi(d0, rs0, ones16), pair_lo(d1, ls0, ones16),
+                                  pair_hi(d1, rs0, ones16));
+        const half8 v1 = as_half8(pair_lo(d0, ls1, ones16), pair_hi(d0, rs1, ones16), pair_lo(d1, ls1, ones16),
+                                  pair_hi(d1, rs1, ones16));
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v0, pop, acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v1, pop, acc[1], 0, 0, 0);
+      }
+      const uint32_t wmj = j == 0 ? wm0 : (j == 1 ? wm1 : (j == 2 ? wm2 : wm3));
+      if (wmj != 0u) {
+        const _Float16* pwr = &B.pw[j][col * kPRow + 8 * g];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const half8 pwop = *reinterpret_cast<const half8*>(pwr + 16 * s2);
+#pragma unroll
+          for (int b = 0; b < 2; ++b)
+            acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vim[j][b][s2], pwop, acc[b], 0, 0, 0);
+        }
+      }
+    }
+  };
+
+  // Steady state: the next step's loads are issued before this step's are
+  // used, unconditionally, so each wait counts exactly one step's loads.
+  int k = 0;
+#pragma unroll 1
+  for (; k + 1 < nst; ++k) {
+    int pgn[kWaves];
+    step_pages(k + 1, pgn);
+    const StepLoad nxt = load_step(a, pgn, (split + nsplit * (k + 1)) * kStepTok, prefix, kvh, w, lane);
+    run_step(cur, k, pg);
+    cur = nxt;
+#pragma unroll
+    for (int j = 0; j < kWaves; ++j) pg[j] = pgn[j];
   }
-  __syncthreads();
-  switch (w) {
-    case 0: rs_recv1_send2<0>(st.acc, f4, off, cb, lane); break;
-    case 1: rs_recv1_send2<1>(st.acc, f4, off, cb, lane); break;
-    case 2: rs_recv1_send2<2>(st.acc, f4, off, cb, lane); break;
-    default: rs_recv1_send2<3>(st.acc, f4, off, cb, lane); break;
+  run_step(cur, k, pg);
+
+  // ---- row sums over both lane halves and the four waves, then the partial ----
+  l_run += shfl_xor_f32(l_run, 32);
+  z_run += shfl_xor_f32(z_run, 32);
+  ps_run += shfl_xor_f32(ps_run, 32);
+  lds_barrier();                                  // the step buffers are free from here on
+  float* red = reinterpret_cast<float*>(&S.buf[0]);
+  if (g == 0) {
+    red[(w * 3 + 0) * kRows + col] = l_run;
+    red[(w * 3 + 1) * kRows + col] = z_run;
+    red[(w * 3 + 2) * kRows + col] = ps_run;
   }
-  __syncthreads();
-  // Round 1's buffers are free now: each wave stages its [32][64] block
-  // there and writes whole 256-byte row segments (16 lanes per row).
-  float* tb = cb;
-  switch (w) {
-    case 0: rs_recv2_stage<0>(st.acc, cb, tb, lane); break;
-    case 1: rs_recv2_stage<1>(st.acc, cb, tb, lane); break;
-    case 2: rs_recv2_stage<2>(st.acc, cb, tb, lane); break;
-    default: rs_recv2_stage<3>(st.acc, cb, tb, lane); break;
+  lds_barrier();
+  float lt = 0.f, zt = 0.f, pt = 0.f;
+#pragma unroll
+  for (int ww = 0; ww < kWaves; ++ww) {
+    lt += red[(ww * 3 + 0) * kRows + col];
+    zt += red[(ww * 3 + 1) * kRows + col];
+    pt += red[(ww * 3 + 2) * kRows + col];
+  }
+  // sum_t p (c vs + vz) = 4 * acc - 4 * sum_t P' + sum_t p vz
+  const float off = zt - 4.f * pt;
+  // Register 4jq + i of block b is local feature 16jq + 8g + 4(i >> 1) + 2b +
+  // (i & 1) of row col: staged as [row][64 + 4 pad] fp32.
+  float* tbuf = red + kWaves * 3 * kRows + w * kTFloats;
+#pragma unroll
+  for (int jq = 0; jq < 4; ++jq) {
+    float* d = tbuf + col * kTRow + 16 * jq + 8 * g;
+    *reinterpret_cast<floatx4*>(d) =
+        floatx4{fmaf(4.f, acc[0][4 * jq], off), fmaf(4.f, acc[0][4 * jq + 1], off),
+                fmaf(4.f, acc[1][4 * jq], off), fmaf(4.f, acc[1][4 * jq + 1], off)};
+    *reinterpret_cast<floatx4*>(d + 4) =
+        floatx4{fmaf(4.f, acc[0][4 * jq + 2], off), fmaf(4.f, acc[0][4 * jq + 3], off),
+                fmaf(4.f, acc[1][4 * jq + 2], off), fmaf(4.f, acc[1][4 * jq + 3], off)};
   }
   wave_sync_lds();
   const int nrow = min(kRows, rows - rt * kRows);
@@ -849,19 +754,14 @@ __global__ __launch_bounds__(256) void paged_decode_split_kernel(DecodeArgs a) {
     const int row = 4 * s4 + (lane >> 4);
     if (row < nrow)
       *reinterpret_cast<floatx4*>(part + row * kHeadDim + 64 * w + 4 * (lane & 15)) =
-          *reinterpret_cast<const floatx4*>(tb + w * kTFloats + row * kTRow + 4 * (lane & 15));
+          *reinterpret_cast<const floatx4*>(tbuf + row * kTRow + 4 * (lane & 15));
   }
   if (w == 0 && lane < nrow) {
-    float lsum = 0.f;
-#pragma unroll
-    for (int k = 0; k < kWaves; ++k) {
-      const float mk = S.mrow[k][lane];
-      if (mk != -__builtin_inff()) lsum += S.lrow[k][lane] * exp2f(mk - mx);
-    }
-    part[kPartO + lane] = mx;
-    part[kPartO + kRows + lane] = lsum;
+    part[kPartO + lane] = m_run;
+    part[kPartO + kRows + lane] = lt;
   }
-  // @probe:5
+  // (a condition that never holds: keeps the page-touching loads alive)
+  if (a.stage_rows < 0 && touched == 0x5EEDu) part[kPartO] = 0.f;
 }
 
 // One 256-thread block per (output row, quarter of the features) of an item.
@@ -889,8 +789,8 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int sg = tid >> 4, fl = tid & 15;
-  const int tiles = (it.prefix + kTile - 1) / kTile;
-  const int hs = min(a.max_splits, tiles);        // history partials 0 .. hs - 1
+  const int steps = (it.prefix + kStepTok - 1) / kStepTok;
+  const int hs = min(a.max_splits, steps);        // history partials 0 .. hs - 1
   const int P = hs + 1;                           // partial hs is the fresh one (split max_splits)
   const float* base = a.ws + item_index(a, item, 0, rt) * kPartialFloats;
   const int64_t pstride = (int64_t)a.row_tiles * kPartialFloats;
@@ -989,13 +889,13 @@ int64_t splits_for(int64_t max_history, int tiles_per_split) {
 }
 
 int default_tiles_per_split(int32_t num_requests, int32_t num_kv_heads, int64_t max_history) {
-  // Enough workgroups to cover the GPU for one long request, few enough that
-  // the partials stay a fraction of the INT2 bytes read, and never more
-  // splits than the merge takes.
+  // Enough workgroups to cover the GPU for one long request (two per CU),
+  // few enough that each runs several steps and the partials stay a fraction
+  // of the INT2 bytes read, and never more splits than the merge takes.
   const int64_t tiles = max_history > 0 ? (max_history + kTile - 1) / kTile : 0;
   const int64_t work = tiles * num_requests * num_kv_heads;
   int tps = 4;
-  while (tps < 64 && work / tps > 1024) tps *= 2;
+  while (tps < 64 && work / tps > 512) tps *= 2;
   while (tps < kMaxTilesPerSplit && (tiles + tps - 1) / tps > kMaxSplits) tps *= 2;
   return tps;
 }

@@ -16,11 +16,12 @@
 // reads for window-owned tokens, per (arena row, 32-token tile, kv head):
 //   K image [16 k-steps m][64 lanes][8 slots]: lane t + 32g, slot 2i + b of
 //     step m = 2j + a holds feature 128g + 16j + 4a + i + 8b of token t;
-//   V image [2 h][4 sp][2 mm][64 lanes][8 slots]: lane c + 32gs holds feature
-//     4(32h + c) + sp; slot 4hi + {0, 2, 1, 3}[w] holds token 16mm + 8hi +
-//     4gs + w.
-// Both are exactly the MFMA operand registers of a wavefront, so the decode
-// copies them to LDS with 16-byte-per-lane direct loads.
+//   V image [4 q][2 b][2 s][64 lanes][8 slots]: lane m + 32gs holds feature
+//     64q + 4(m >> 1) + 2b + (m & 1); slot u holds token 16s + 8gs +
+//     {0, 2, 1, 3, 4, 6, 5, 7}[u].
+// Both are exactly MFMA operand registers of the decode's wavefronts (K: the
+// tile's owner, V: wavefront q's quarter of the features), which read them
+// with one 16-byte load per lane and block.
 #include "oscar_common.h"
 
 namespace oscar {
@@ -59,10 +60,10 @@ __device__ __forceinline__ int kimg_offset(int f, int t) {
 }
 
 __device__ __forceinline__ int vimg_offset(int f, int t) {
-  const int c = (f >> 2) & 31, h = f >> 7, sp = f & 3;
-  const int mm = t >> 4, t16 = t & 15, gs = (t16 & 7) >> 2, hi = t16 >> 3, wq = t & 3;
-  const int slot = 4 * hi + (wq == 1 ? 2 : (wq == 2 ? 1 : wq));
-  return ((((h * 4 + sp) * 2 + mm) * 64) + c + 32 * gs) * 8 + slot;
+  const int q = f >> 6, b = (f >> 1) & 1, m = 2 * ((f >> 2) & 15) + (f & 1);
+  const int s = t >> 4, gs = (t >> 3) & 1, r = t & 7;
+  const int slot = r == 1 ? 2 : (r == 2 ? 1 : (r == 5 ? 6 : (r == 6 ? 5 : r)));   // self-inverse
+  return ((((q * 2 + b) * 2 + s) * 64) + m + 32 * gs) * 8 + slot;
 }
 
 __device__ __forceinline__ int64_t seat_of(int64_t slot, const StageArgs& a) {

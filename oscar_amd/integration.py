@@ -57,7 +57,7 @@ def decode_tiles_per_split(max_requests: int, num_kv_heads: int, max_history: in
     tiles = -(-max_history // DECODE_TILE) if max_history > 0 else 0
     work = tiles * max_requests * num_kv_heads
     tps = 4
-    while tps < 64 and work // tps > 1024:
+    while tps < 64 and work // tps > 512:
         tps *= 2
     while tps < DECODE_MAX_TILES_PER_SPLIT and -(-tiles // tps) > DECODE_MAX_SPLITS:
         tps *= 2

@@ -32,11 +32,11 @@ def _k_image_order() -> torch.Tensor:
 
 
 def _v_image_tokens() -> torch.Tensor:
-    """Token at (mm, gs, u) of the V image: 16mm + 4gs + (0, 2, 1, 3, 8, 10, 9, 11)[u]."""
-    order = torch.tensor([0, 2, 1, 3, 8, 10, 9, 11])
-    mm = torch.arange(2).view(2, 1, 1)
+    """Token at (s, gs, u) of the V image: 16s + 8gs + (0, 2, 1, 3, 4, 6, 5, 7)[u]."""
+    order = torch.tensor([0, 2, 1, 3, 4, 6, 5, 7])
+    s = torch.arange(2).view(2, 1, 1)
     gs = torch.arange(2).view(1, 2, 1)
-    return (16 * mm + 4 * gs + order.view(1, 1, 8)).reshape(-1)
+    return (16 * s + 8 * gs + order.view(1, 1, 8)).reshape(-1)
 
 
 def image_shape(rows: int, bs: int, hk: int) -> tuple:
@@ -46,7 +46,8 @@ def image_shape(rows: int, bs: int, hk: int) -> tuple:
 def stage_images(stage_k: torch.Tensor, stage_v: torch.Tensor):
     """fp16 operand images of a whole arena (the layout oscar_staging_write
     maintains incrementally): K [rows][bs/32][Hk][m][lane = t + 32g][slot],
-    V [rows][bs/32][Hk][h][sp][mm][lane = c + 32gs][slot]."""
+    V [rows][bs/32][Hk][q][b][s][lane = m + 32gs][slot] with feature
+    64q + 4(m // 2) + 2b + m % 2."""
     rows, bs, hk, d = stage_k.shape
     if d != 256 or bs % 32:
         raise ValueError("operand images need D = 256 and a block size that is a multiple of 32")
@@ -56,9 +57,9 @@ def stage_images(stage_k: torch.Tensor, stage_v: torch.Tensor):
     x = x.view(rows, T, 32, hk, 2, 16, 8).permute(0, 1, 3, 5, 4, 2, 6)      # [r, T, hk, m, g, t, u]
     kimg = x.reshape(rows, T, hk, IMAGE_HALFS).contiguous()
     y = stage_v.view(rows, T, 32, hk, d).to(torch.float16).permute(0, 1, 3, 4, 2)  # [r, T, hk, f, tok]
-    y = y[..., _v_image_tokens().to(dev)]                                    # [r, T, hk, f, (mm, gs, u)]
-    y = y.reshape(rows, T, hk, 2, 32, 4, 2, 2, 8)                           # f = (h, c, sp)
-    y = y.permute(0, 1, 2, 3, 5, 6, 7, 4, 8)                                 # [r, T, hk, h, sp, mm, gs, c, u]
+    y = y[..., _v_image_tokens().to(dev)]                                    # [r, T, hk, f, (s, gs, u)]
+    y = y.reshape(rows, T, hk, 4, 16, 2, 2, 2, 2, 8)                        # f = (q, bl, b, e)
+    y = y.permute(0, 1, 2, 3, 5, 7, 8, 4, 6, 9)                              # [r, T, hk, q, b, s, gs, (bl, e), u]
     vimg = y.reshape(rows, T, hk, IMAGE_HALFS).contiguous()
     return kimg, vimg
 

@@ -246,3 +246,34 @@ def test_plan_capacity_fits_one_mi355x():
     assert plan["tokens"] == plan["blocks"] * 128
     # one INT2 token of one layer costs 2 * 256 bytes of int8-geometry slots
     assert plan["native_per_block"] == 2 * 128 * 256 * 16
+
+
+def test_operand_image_layouts_follow_their_formulas():
+    """The fp16 window images the decode reads as MFMA operands, element by element:
+    K block m, lane t + 32g, slot u = feature 128g + 16(m // 2) + 4(m % 2) + u // 2 + 8(u % 2)
+    of token t; V block (q, b, s), lane m + 32gs, slot u = feature 64q + 4(m // 2) + 2b + m % 2
+    of token 16s + 8gs + (0, 2, 1, 3, 4, 6, 5, 7)[u]."""
+    from oscar_amd.kernels import staging as kstaging
+
+    g = torch.Generator().manual_seed(3)
+    sk = torch.randn(2, 64, 1, 256, generator=g)
+    sv = torch.randn(2, 64, 1, 256, generator=g)
+    kimg, vimg = kstaging.stage_images(sk, sv)
+    order = [0, 2, 1, 3, 4, 6, 5, 7]
+    for r, tile in ((0, 0), (1, 1)):
+        K = kimg[r, tile, 0].view(16, 64, 8)
+        V = vimg[r, tile, 0].view(4, 2, 2, 64, 8)
+        for lane in range(64):
+            t, gg = lane % 32, lane // 32
+            for m in range(16):
+                for u in range(8):
+                    f = 128 * gg + 16 * (m // 2) + 4 * (m % 2) + u // 2 + 8 * (u % 2)
+                    assert K[m, lane, u] == sk[r, 32 * tile + t, 0, f].half()
+            mm, gs = lane % 32, lane // 32
+            for q in range(4):
+                for b in range(2):
+                    for s in range(2):
+                        for u in range(8):
+                            f = 64 * q + 4 * (mm // 2) + 2 * b + mm % 2
+                            tok = 16 * s + 8 * gs + order[u]
+                            assert V[q, b, s, lane, u] == sv[r, 32 * tile + tok, 0, f].half()
