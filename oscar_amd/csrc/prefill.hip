@@ -10,11 +10,18 @@
 // tolerance even on x8 outlier channels.  Accumulation and softmax are fp32.
 // Rotated domain in, rotated-V domain out (fp32).
 //
-// One block of 4 wavefronts per 128 consecutive rows of one kv-head, a row
-// being (new token j, head-in-group).  For every 32-key block the 256 threads
-// produce K (token-major) and V (feature-major) fp16 tiles in LDS; each wave
-// then runs S^T = K Q^T (16 MFMA 32x32x16) and O^T += V^T P^T (16 MFMA) on
-// its 32 rows with base-2 online softmax.
+// One workgroup per 128 consecutive rows of one kv-head, a row being (new
+// token j, head-in-group); workgroups of later rows (more keys) are
+// dispatched first.  Keys are walked in 32-key blocks through two LDS tile
+// buffers, history blocks first, then new-token blocks.  Waves 4-7 produce:
+// the raw loads of block i + 2 (codes, meta, owner tags, or the new tokens'
+// fp32 values) are in flight while block i + 1's become fp16 K (token-major)
+// and V (feature-major) tiles.  Waves 0-3 consume, 32 rows each: S^T = K Q^T
+// (16 MFMA 32x32x16, two accumulator chains, Q^T from LDS) and O^T += V^T
+// P^T (16 MFMA) with base-2 online softmax and a lazily raised running max.
+// One barrier per block hands a buffer from producers to consumers; a
+// producer wave and a consumer wave share each SIMD, so dequantization
+// overlaps the MFMAs.
 #include "oscar_common.h"
 
 namespace oscar {
@@ -24,8 +31,10 @@ constexpr int kBlk = 32;
 constexpr int kRowsPerWave = 32;
 constexpr int kWaves = 4;
 constexpr int kKs = kHeadDim + 8;     // halfs per K row in LDS
-constexpr int kVs = kBlk + 8;         // halfs per V feature row in LDS
+constexpr int kVs = kBlk + 4;         // halfs per V feature row in LDS (72 B: 8-byte reads conflict-free)
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazy = 8.f;          // log2 headroom before a running max is raised
 
 struct PrefillArgs {
   const float* q;        // [N][Hq][D]
@@ -49,69 +58,305 @@ struct PrefillArgs {
   float* out;
 };
 
+// Two key blocks of fp16 tiles: block k is computed from one while block
+// k + 1 is written into the other.
+struct PrefillLds {
+  _Float16 kh[2][kBlk * kKs];           // K token-major
+  _Float16 vt[2][kHeadDim * kVs];       // V feature-major
+  _Float16 q[kWaves][16 * 2 * kRowsPerWave * 8];   // Q^T operands [wave][m][g][row][8]
+};
+constexpr size_t kPrefillLds = sizeof(PrefillLds);
+static_assert(kPrefillLds <= 160 * 1024, "LDS of one workgroup");
+
 __device__ __forceinline__ _Float16 to_h(float x) { return (_Float16)x; }
 
-// Resolve history position p (< C): page, row in page, staging seat (or -1).
-struct HistLoc {
-  int64_t page;
-  int32_t prow;
-  int64_t seat;   // >= 0: read FP32 staging
-  bool ok;
-};
-
-__device__ __forceinline__ HistLoc locate(const PrefillArgs& a, int64_t p) {
-  HistLoc h{0, 0, -1, false};
-  const int64_t pidx = p / a.block_size;
-  if (pidx >= a.bt_cols) return h;
-  const int64_t page = a.bt[pidx];
-  if (page < 0 || page >= a.num_pages) return h;
-  h.page = page;
-  h.prow = (int32_t)(p - pidx * a.block_size);
-  h.ok = true;
-  if (a.stage_rows > 0) {
-    const int64_t seat = (page % a.stage_rows) * a.block_size + h.prow;
-    if (a.owner[seat] == page) h.seat = seat;
-  }
-  return h;
+// s_barrier without __syncthreads' memory fence (which would also wait for
+// the producers' outstanding global loads); LDS writes are complete at
+// lgkmcnt(0).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);       // lgkmcnt(0); vmcnt and expcnt left at their maxima
+  asm volatile("s_barrier" ::: "memory");
 }
 
-__global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) _Float16 kh[kBlk * kKs];
-  __shared__ __attribute__((aligned(16))) _Float16 vt[kHeadDim * kVs];
+__device__ __forceinline__ void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
+// The key blocks a workgroup walks: first the history blocks (keys < C, in
+// 32-key blocks from 0), then the new-token blocks (from the block holding
+// key C).  A block that straddles C is walked twice, each time with the
+// other side's keys masked out.
+struct BlockPlan {
+  int64_t n_hist;     // history blocks
+  int64_t n_new;      // new-token blocks
+  int64_t new0;       // first key of the first new-token block
+};
+
+__device__ __forceinline__ BlockPlan block_plan(int64_t C, int64_t keys) {
+  BlockPlan b;
+  b.n_hist = (C + kBlk - 1) / kBlk;
+  b.new0 = (C / kBlk) * kBlk;
+  b.n_new = keys > C ? (keys - b.new0 + kBlk - 1) / kBlk : 0;
+  return b;
+}
+
+// Raw loads of one history block for one producer thread: K role (token ktt,
+// features 32 kfg .. +31) k = {codes lo, codes hi, meta, owner}; V role
+// (tokens 8 vtg + w, features 4 vfg .. +3) v[w] = {code byte, V meta, owner}.
+// Every thread issues all 27 loads whatever the block holds (tokens past C
+// and invalid pages read an in-bounds slot, masked later), so a wait counts
+// exactly one block's loads.
+struct HistLoad {
+  u32x4 k;
+  uint32_t vb[8], vm[8], vo[8];
+};
+
+// Raw loads of one new-token block: K role k[i] = fp32 values 32 kfg + 4i ..,
+// V role v[w] = fp32 values 4 vfg .. +3 of token 8 vtg + w (16 loads, indices
+// clamped into range, masked later).
+struct NewLoad {
+  floatx4 k[8];
+  floatx4 v[8];
+};
+
+__device__ __forceinline__ int32_t block_page(const PrefillArgs& a, int64_t k0) {
+  const int64_t pidx = k0 / a.block_size;
+  const int32_t p = (k0 < a.cached && pidx < a.bt_cols) ? a.bt[pidx] : -1;
+  return p;
+}
+
+__device__ __forceinline__ HistLoad load_hist(const PrefillArgs& a, int64_t k0, int32_t page, int kvh, int ktt,
+                                              int kfg, int vtg, int vfg) {
+  HistLoad L;
+  const bool page_ok = page >= 0 && page < a.num_pages;
+  const int64_t pg = page_ok ? page : 0;
+  const uint8_t* kpage = a.k_cache + pg * a.k_page + (int64_t)kvh * a.k_head;
+  const uint8_t* vpage = a.v_cache + pg * a.v_page + (int64_t)kvh * a.v_head;
+  // Owner tags are pages (< 2^31) or -1: the low word of the little-endian
+  // int64 identifies them.  Without an arena the K slot's meta stands in.
+  const int32_t* opage = a.stage_rows > 0 ? reinterpret_cast<const int32_t*>(
+                                                a.owner + (pg % a.stage_rows) * a.block_size)
+                                          : reinterpret_cast<const int32_t*>(kpage);
+  const int ostride = a.stage_rows > 0 ? 2 : 0;
+  const int prow0 = (int)(k0 % a.block_size);
+  const uint32_t ktok = (uint32_t)a.k_tok, vtok = (uint32_t)a.v_tok;
+  {
+    const int row = prow0 + ktt;
+    const uint8_t* ks = kpage + (uint32_t)row * ktok;
+    const u32x2 cw = *reinterpret_cast<const u32x2*>(ks + kKCodeOff + 8 * kfg);
+    L.k[0] = cw[0];
+    L.k[1] = cw[1];
+    L.k[2] = *reinterpret_cast<const uint32_t*>(ks);
+    L.k[3] = (uint32_t)opage[ostride * row];
+  }
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    const int row = prow0 + 8 * vtg + w;
+    L.vb[w] = vpage[(uint32_t)row * vtok + vfg];
+    L.vm[w] = *reinterpret_cast<const uint32_t*>(kpage + (uint32_t)row * ktok + 4);
+    L.vo[w] = (uint32_t)opage[ostride * row];
+  }
+  return L;
+}
+
+__device__ __forceinline__ NewLoad load_new(const PrefillArgs& a, int64_t k0, int kvh, int ktt, int kfg, int vtg,
+                                            int vfg) {
+  NewLoad L;
+  const int64_t C = a.cached, N = a.n_new;
+  const int64_t hs = (int64_t)a.num_kv_heads * kHeadDim;
+  {
+    const int64_t j = min(max(k0 + ktt - C, (int64_t)0), N - 1);
+    const floatx4* src = reinterpret_cast<const floatx4*>(a.k_new + j * hs + kvh * kHeadDim + 32 * kfg);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) L.k[i] = src[i];
+  }
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    const int64_t j = min(max(k0 + 8 * vtg + w - C, (int64_t)0), N - 1);
+    L.v[w] = *reinterpret_cast<const floatx4*>(a.v_new + j * hs + kvh * kHeadDim + 4 * vfg);
+  }
+  return L;
+}
+
+__device__ __forceinline__ void store_tiles(const float (&kv)[32], const float (&vv)[4][8], int ktt, int kfg,
+                                            int vtg, int vfg, _Float16* kh, _Float16* vt) {
+  half8* dst = reinterpret_cast<half8*>(kh + ktt * kKs + 32 * kfg);
+#pragma unroll
+  for (int q8 = 0; q8 < 4; ++q8) {
+    half8 x;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = to_h(kv[8 * q8 + e]);
+    dst[q8] = x;
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    half4 lo, hi;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      lo[w] = to_h(vv[u][w]);
+      hi[w] = to_h(vv[u][4 + w]);
+    }
+    half4* d = reinterpret_cast<half4*>(vt + (4 * vfg + u) * kVs + 8 * vtg);
+    d[0] = lo;
+    d[1] = hi;
+  }
+}
+
+// History tiles: c * s + z in fp32, rounded once to fp16; tokens the staging
+// arena owns are reloaded from it (rare: the sink / recent window).  Keys
+// past C or on an invalid page become whatever the loads held: the consumer
+// masks them.
+__device__ __forceinline__ void store_hist(const PrefillArgs& a, const HistLoad& L, int64_t k0, int32_t page,
+                                           int kvh, int ktt, int kfg, int vtg, int vfg, _Float16* kh,
+                                           _Float16* vt) {
+  const bool arena = a.stage_rows > 0 && page >= 0 && page < a.num_pages;
+  const int64_t seat0 = arena ? (int64_t)(page % a.stage_rows) * a.block_size : 0;
+  const int prow0 = (int)(k0 % a.block_size);
+  float kv[32];
+  float vv[4][8];
+  {
+    const float sc = f16_bits_to_f32(L.k[2]), zr = f16_bits_to_f32(L.k[2] >> 16);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      kv[u] = (float)((L.k[0] >> (2 * u)) & 3u) * sc + zr;
+      kv[16 + u] = (float)((L.k[1] >> (2 * u)) & 3u) * sc + zr;
+    }
+    if (arena && (int32_t)L.k[3] == page) {
+      const floatx4* src = reinterpret_cast<const floatx4*>(
+          a.stage_k + ((seat0 + prow0 + ktt) * a.num_kv_heads + kvh) * kHeadDim + 32 * kfg);
+#pragma unroll
+      for (int q4 = 0; q4 < 8; ++q4) {
+        const floatx4 x = src[q4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kv[4 * q4 + e] = x[e];
+      }
+    }
+  }
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    const float sc = f16_bits_to_f32(L.vm[w]), zr = f16_bits_to_f32(L.vm[w] >> 16);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) vv[u][w] = (float)((L.vb[w] >> (2 * u)) & 3u) * sc + zr;
+    if (arena && (int32_t)L.vo[w] == page) {
+      const floatx4 y = *reinterpret_cast<const floatx4*>(
+          a.stage_v + ((seat0 + prow0 + 8 * vtg + w) * a.num_kv_heads + kvh) * kHeadDim + 4 * vfg);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) vv[u][w] = y[u];
+    }
+  }
+  if (!(page >= 0 && page < a.num_pages)) {     // an unmapped page reads as zeros
+#pragma unroll
+    for (int u = 0; u < 32; ++u) kv[u] = 0.f;
+#pragma unroll
+    for (int w = 0; w < 8; ++w)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) vv[u][w] = 0.f;
+  }
+  store_tiles(kv, vv, ktt, kfg, vtg, vfg, kh, vt);
+}
+
+__device__ __forceinline__ void store_new(const NewLoad& L, int ktt, int kfg, int vtg, int vfg, _Float16* kh,
+                                          _Float16* vt) {
+  float kv[32];
+  float vv[4][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) kv[4 * i + e] = L.k[i][e];
+#pragma unroll
+  for (int w = 0; w < 8; ++w)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) vv[u][w] = L.v[w][u];
+  store_tiles(kv, vv, ktt, kfg, vtg, vfg, kh, vt);
+}
+
+// 8 wavefronts: waves 0-3 compute (32 rows each), waves 4-7 produce the
+// fp16 tiles of the next key block, two blocks of loads ahead.
+__global__ __launch_bounds__(512, 1) void prefill_kernel(PrefillArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
+  PrefillLds& S = *reinterpret_cast<PrefillLds*>(smem_raw);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool producer = wave >= kWaves;
   const int g = lane >> 5;
   const int col = lane & 31;
   const int kvh = blockIdx.y;
   const int64_t rows_total = (int64_t)a.n_new * a.group;
-  const int64_t row0 = (int64_t)blockIdx.x * (kWaves * kRowsPerWave);
+  // Blocks of later rows see more keys: they are dispatched first.
+  const int64_t row0 = (int64_t)(gridDim.x - 1 - blockIdx.x) * (kWaves * kRowsPerWave);
+  const int64_t C = a.cached;
+  const int64_t last_row = min(row0 + kWaves * kRowsPerWave, rows_total) - 1;
+  const int64_t keys_blk = C + last_row / a.group + 1;
+  const BlockPlan plan = block_plan(C, keys_blk);
+  const int64_t nblk = plan.n_hist + plan.n_new;
+  auto block_k0 = [&](int64_t i) { return i < plan.n_hist ? i * kBlk : plan.new0 + (i - plan.n_hist) * kBlk; };
+
+  if (producer) {
+    const int ptid = tid - kWaves * 64;
+    const int ktt = ptid >> 3, kfg = ptid & 7;       // K: token ktt, features 32*kfg .. +31
+    const int vtg = ptid >> 6, vfg = ptid & 63;      // V: tokens 8*vtg .. +7, features 4*vfg .. +3
+    // History pass: loads of block i + 2 out while block i + 1's are turned
+    // into tiles; then the same for the new-token pass.
+    const int64_t nh = plan.n_hist;
+    int32_t pg_a = block_page(a, 0), pg_b = block_page(a, kBlk);
+    int64_t i = 0;
+    if (nh > 0) {
+      HistLoad La = load_hist(a, 0, pg_a, kvh, ktt, kfg, vtg, vfg);
+      HistLoad Lb = load_hist(a, kBlk, pg_b, kvh, ktt, kfg, vtg, vfg);
+      int32_t pg_c = block_page(a, 2 * kBlk);
+#pragma unroll 1
+      for (; i < nh; ++i) {
+        store_hist(a, La, i * kBlk, pg_a, kvh, ktt, kfg, vtg, vfg, S.kh[i & 1], S.vt[i & 1]);
+        La = Lb;
+        pg_a = pg_b;
+        Lb = load_hist(a, (i + 2) * kBlk, pg_c, kvh, ktt, kfg, vtg, vfg);
+        pg_b = pg_c;
+        pg_c = block_page(a, (i + 3) * kBlk);
+        lds_barrier();        // tiles of block i ready / block i - 1 consumed
+      }
+    }
+    if (plan.n_new > 0) {
+      NewLoad La = load_new(a, plan.new0, kvh, ktt, kfg, vtg, vfg);
+      NewLoad Lb = load_new(a, plan.new0 + kBlk, kvh, ktt, kfg, vtg, vfg);
+#pragma unroll 1
+      for (; i < nblk; ++i) {
+        store_new(La, ktt, kfg, vtg, vfg, S.kh[i & 1], S.vt[i & 1]);
+        La = Lb;
+        Lb = load_new(a, block_k0(i) + 2 * kBlk, kvh, ktt, kfg, vtg, vfg);
+        lds_barrier();
+      }
+    }
+    lds_barrier();            // the consumers' last block
+    return;
+  }
+
+  // ---- consumers: 32 rows per wave ----
   const int64_t wrow0 = row0 + wave * kRowsPerWave;
   const int64_t row = wrow0 + col;
   const bool row_ok = row < rows_total;
-  const int64_t C = a.cached;
-
-  // Key range of the block: up to the last row's causal limit.
-  const int64_t last_row = min(row0 + kWaves * kRowsPerWave, rows_total) - 1;
-  const int64_t keys_blk = C + last_row / a.group + 1;
   const int64_t wave_last = min(wrow0 + kRowsPerWave, rows_total) - 1;
   const int64_t keys_wave = wrow0 < rows_total ? C + wave_last / a.group + 1 : 0;
   const int64_t my_limit = row_ok ? C + row / a.group : -1;   // last visible key
-
-  half8 qop[16];
   {
+    // Q^T operands of the wave's rows: lane (row col, half g) holds features
+    // 16m + 8g .. +7 of k-step m.
     const int64_t j = row_ok ? row / a.group : 0;
     const int h = kvh * a.group + (row_ok ? (int)(row % a.group) : 0);
     const float* qp = a.q + (j * a.num_heads + h) * kHeadDim + 8 * g;
+    _Float16* qdst = S.q[wave] + (g * kRowsPerWave + col) * 8;
 #pragma unroll
     for (int m = 0; m < 16; ++m) {
       floatx4 x0 = row_ok ? *reinterpret_cast<const floatx4*>(qp + 16 * m) : floatx4{};
       floatx4 x1 = row_ok ? *reinterpret_cast<const floatx4*>(qp + 16 * m + 4) : floatx4{};
-      qop[m] = half8{to_h(x0[0]), to_h(x0[1]), to_h(x0[2]), to_h(x0[3]),
-                      to_h(x1[0]), to_h(x1[1]), to_h(x1[2]), to_h(x1[3])};
+      *reinterpret_cast<half8*>(qdst + m * 2 * kRowsPerWave * 8) =
+          half8{to_h(x0[0]), to_h(x0[1]), to_h(x0[2]), to_h(x0[3]),
+                to_h(x1[0]), to_h(x1[1]), to_h(x1[2]), to_h(x1[3])};
     }
   }
+  wave_sync_lds();
 
   floatx16 acc[8];
 #pragma unroll
@@ -119,145 +364,74 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   float m_run = -__builtin_inff();
   float l_run = 0.f;
 
-  // Producer roles.
-  const int ktt = tid >> 3, kfg = tid & 7;       // K: token ktt, features 32*kfg .. +31
-  const int vtg = tid >> 6, vfg = tid & 63;      // V: tokens 8*vtg .. +7, features 4*vfg .. +3
-
 #pragma unroll 1
-  for (int64_t k0 = 0; k0 < keys_blk; k0 += kBlk) {
-    // ---------------- K tile ----------------
-    {
-      const int64_t p = k0 + ktt;
-      float kv[32];
-#pragma unroll
-      for (int u = 0; u < 32; ++u) kv[u] = 0.f;
-      if (p < C) {
-        const HistLoc h = locate(a, p);
-        if (h.ok && h.seat >= 0) {
-          const floatx4* src = reinterpret_cast<const floatx4*>(
-              a.stage_k + (h.seat * a.num_kv_heads + kvh) * kHeadDim + 32 * kfg);
-#pragma unroll
-          for (int q4 = 0; q4 < 8; ++q4) {
-            const floatx4 x = src[q4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) kv[4 * q4 + e] = x[e];
-          }
-        } else if (h.ok) {
-          const uint8_t* ks = a.k_cache + h.page * a.k_page + h.prow * a.k_tok + kvh * a.k_head;
-          const uint32_t meta = *reinterpret_cast<const uint32_t*>(ks);
-          const u32x2 cw = *reinterpret_cast<const u32x2*>(ks + kKCodeOff + 8 * kfg);
-          const float sc = f16_bits_to_f32(meta), zr = f16_bits_to_f32(meta >> 16);
-#pragma unroll
-          for (int u = 0; u < 16; ++u) {
-            kv[u] = (float)((cw[0] >> (2 * u)) & 3u) * sc + zr;
-            kv[16 + u] = (float)((cw[1] >> (2 * u)) & 3u) * sc + zr;
-          }
-        }
-      } else if (p < C + a.n_new) {
-        const floatx4* src = reinterpret_cast<const floatx4*>(
-            a.k_new + ((p - C) * a.num_kv_heads + kvh) * kHeadDim + 32 * kfg);
-#pragma unroll
-        for (int q4 = 0; q4 < 8; ++q4) {
-          const floatx4 x = src[q4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) kv[4 * q4 + e] = x[e];
-        }
-      }
-      half8* dst = reinterpret_cast<half8*>(kh + ktt * kKs + 32 * kfg);
-#pragma unroll
-      for (int q8 = 0; q8 < 4; ++q8) {
-        half8 x;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = to_h(kv[8 * q8 + e]);
-        dst[q8] = x;
-      }
-    }
-    // ---------------- V tile (feature-major) ----------------
-    {
-      float vv[4][8];
-#pragma unroll
-      for (int w = 0; w < 8; ++w) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) vv[u][w] = 0.f;
-        const int64_t p = k0 + 8 * vtg + w;
-        if (p < C) {
-          const HistLoc h = locate(a, p);
-          if (h.ok && h.seat >= 0) {
-            const floatx4 x = *reinterpret_cast<const floatx4*>(
-                a.stage_v + (h.seat * a.num_kv_heads + kvh) * kHeadDim + 4 * vfg);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) vv[u][w] = x[u];
-          } else if (h.ok) {
-            const uint8_t* ks = a.k_cache + h.page * a.k_page + h.prow * a.k_tok + kvh * a.k_head;
-            const uint8_t* vs = a.v_cache + h.page * a.v_page + h.prow * a.v_tok + kvh * a.v_head;
-            const uint32_t meta = *reinterpret_cast<const uint32_t*>(ks + 4);
-            const uint32_t cb = vs[vfg];
-            const float sc = f16_bits_to_f32(meta), zr = f16_bits_to_f32(meta >> 16);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) vv[u][w] = (float)((cb >> (2 * u)) & 3u) * sc + zr;
-          }
-        } else if (p < C + a.n_new) {
-          const floatx4 x = *reinterpret_cast<const floatx4*>(
-              a.v_new + ((p - C) * a.num_kv_heads + kvh) * kHeadDim + 4 * vfg);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) vv[u][w] = x[u];
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        half8 x;
-#pragma unroll
-        for (int w = 0; w < 8; ++w) x[w] = to_h(vv[u][w]);
-        *reinterpret_cast<half8*>(vt + (4 * vfg + u) * kVs + 8 * vtg) = x;
-      }
-    }
-    __syncthreads();
-
+  for (int64_t i = 0; i < nblk; ++i) {
+    lds_barrier();            // tiles of block i ready
+    const int64_t k0 = block_k0(i);
+    const bool hist = i < plan.n_hist;
     if (k0 < keys_wave) {
-      floatx16 s = floatx16{};
+      const _Float16* kh = S.kh[i & 1];
+      const _Float16* vt = S.vt[i & 1];
+      const half8* qsrc = reinterpret_cast<const half8*>(S.q[wave] + (g * kRowsPerWave + col) * 8);
+      floatx16 s0 = floatx16{}, s1 = floatx16{};
 #pragma unroll
-      for (int m = 0; m < 16; ++m) {
+      for (int m = 0; m < 16; m += 2) {
         const half8 ka = *reinterpret_cast<const half8*>(kh + col * kKs + 16 * m + 8 * g);
-        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qop[m], s, 0, 0, 0);
+        const half8 kb2 = *reinterpret_cast<const half8*>(kh + col * kKs + 16 * (m + 1) + 8 * g);
+        s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qsrc[m * 2 * kRowsPerWave], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kb2, qsrc[(m + 1) * 2 * kRowsPerWave], s1, 0, 0, 0);
       }
+      floatx16 s = s0 + s1;
+      // Visible keys of this pass: history keys < C in the history pass, new
+      // keys >= C in the new-token pass, causal for both.
+      const int64_t lo = hist ? 0 : C;
+      const int64_t hi = hist ? min(C - 1, my_limit) : my_limit;
       float mb = -__builtin_inff();
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t kp = k0 + 8 * (r >> 2) + 4 * g + (r & 3);
-        const float x = (kp <= my_limit) ? s[r] * a.scale_log2 : -__builtin_inff();
+        const float x = (kp >= lo && kp <= hi) ? s[r] * a.scale_log2 : -__builtin_inff();
         s[r] = x;
         mb = fmaxf(mb, x);
       }
       mb = fmaxf(mb, shfl_xor_f32(mb, 32));
-      const float m_new = fmaxf(m_run, mb);
-      float alpha = 1.f;
-      if (m_new != -__builtin_inff()) alpha = (m_run == -__builtin_inff()) ? 0.f : exp2f(m_run - m_new);
+      // Lazy running max: raised only when a block exceeds it by more than
+      // 2^kLazy (probabilities stay <= 2^kLazy, exact range for fp16), and the
+      // first raise of a row needs no rescale.
+      const bool need = mb > m_run + kLazy;
+      const bool resc = need && m_run != -__builtin_inff();
+      if (__ballot(resc)) {
+        const float alpha = resc ? __builtin_amdgcn_exp2f(m_run - mb) : 1.f;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc[t] *= alpha;
+        l_run *= alpha;
+      }
+      if (need) m_run = mb;
+      // exp2(-inf - m) = 0 needs a finite m: rows that have seen no key yet use 0.
+      const float m_use = m_run == -__builtin_inff() ? 0.f : m_run;
       float psum = 0.f;
       half8 pb[2];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = (s[r] == -__builtin_inff()) ? 0.f : exp2f(s[r] - m_new);
+        const float p = __builtin_amdgcn_exp2f(s[r] - m_use);
         psum += p;
         pb[r >> 3][r & 7] = to_h(p);
       }
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) acc[t] *= alpha;
+      l_run += psum;
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
           const _Float16* vrow = vt + (32 * t + col) * kVs + 16 * mm + 4 * g;
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
-          const half8 va = __builtin_bit_cast(half8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+          const u32x2 lo2 = *reinterpret_cast<const u32x2*>(vrow);
+          const u32x2 hi2 = *reinterpret_cast<const u32x2*>(vrow + 8);
+          const half8 va = __builtin_bit_cast(half8, u32x4{lo2[0], lo2[1], hi2[0], hi2[1]});
           acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[mm], acc[t], 0, 0, 0);
         }
       }
     }
-    __syncthreads();
   }
+  lds_barrier();              // pairs with the producers' last barrier
 
   if (!row_ok) return;
   const float l_tot = l_run + shfl_xor_f32(l_run, 32);
@@ -295,7 +469,7 @@ extern "C" int oscar_prefill_continuation(
     return kErrInvalidArgument;
   if (stage_rows > 0 && (!stage_k || !stage_v || !stage_owner)) return kErrInvalidArgument;
   if (k_stride_head < kKCodeOff + kCodeBytes || v_stride_head < kCodeBytes || (k_stride_head & 7) ||
-      (k_stride_token & 7) || (k_stride_page & 7))
+      (k_stride_token & 7) || (k_stride_page & 7) || block_size % kBlk != 0)
     return kErrUnsupportedGeometry;
   PrefillArgs a{};
   a.q = q_rot;
@@ -326,6 +500,13 @@ extern "C" int oscar_prefill_continuation(
   a.out = out;
   const int64_t rows = (int64_t)num_new * a.group;
   dim3 grid((unsigned)((rows + kWaves * kRowsPerWave - 1) / (kWaves * kRowsPerWave)), (unsigned)num_kv_heads);
-  hipLaunchKernelGGL(prefill_kernel, grid, dim3(kWaves * 64), 0, stream, a);
+  static bool lds_attr_set = false;
+  if (!lds_attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPrefillLds) != hipSuccess)
+      return kErrLaunch;
+    lds_attr_set = true;
+  }
+  hipLaunchKernelGGL(prefill_kernel, grid, dim3(2 * kWaves * 64), kPrefillLds, stream, a);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
