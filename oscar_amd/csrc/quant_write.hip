@@ -328,11 +328,12 @@ __global__ __launch_bounds__(256) void quant_write_prerotated_kernel(
 //     f = 128*((r >> 2) & 1) + 16*T + 4*(r >> 3) + (r & 3), r = lane & 31
 //   so that accumulator register i of tile T in lane l is feature
 //   128*(l >> 5) + 16*T + i of token (l & 31) -- the per-lane layout above.
-// grid = (ceil(N / 256), Hk * 2), block = 512 (8 waves x 32 tokens, two per
-// SIMD).  The 16 K-step chunks (16 KB each) stream through a 4-slot LDS ring
-// filled with global_load_lds_dwordx4: chunk m + 3 is requested while chunk m
-// is multiplied, into the slot chunk m - 1 left.  Each K step issues the 8
-// tiles' hi passes, then their lo passes, so no MFMA waits on the previous.
+// grid = (ceil(N / 128), Hk * 2), block = 256 (4 waves x 32 tokens; two
+// blocks per CU).  The 16 K-step chunks (16 KB each) stream through a 4-slot
+// LDS ring filled with global_load_lds_dwordx4: chunk m + 3 is requested
+// while chunk m is multiplied, into the slot chunk m - 1 left.  Each K step
+// issues the 8 tiles' hi passes, then their lo passes, so no MFMA waits on the
+// previous.
 // ---------------------------------------------------------------------------
 constexpr int kFusedWaves = 4;
 constexpr int kChunkBytes = 2 * 8 * 64 * 16;   // one K step: 2 passes x 8 tiles x 64 lanes x 16 B
