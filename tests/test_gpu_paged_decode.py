@@ -97,3 +97,27 @@ def test_invalid_layout_rejected(device):
     with pytest.raises(ValueError):
         decode.paged_attention(q.to(device), k.to(device), v.to(device), case.layer.k_cache.to(device),
                                case.layer.v_cache.to(device), case.bt.to(device), [0, 2], [1], 0.0625)
+
+
+@pytest.mark.parametrize("bs", [32, 128])
+@pytest.mark.parametrize("tiles_per_split", [8, 32, 256])
+def test_multi_step_splits_with_window(device, bs, tiles_per_split):
+    """Workgroups that walk several 128-token steps (prefetched loads, double-buffered
+    step buffers, window steps in the middle of a workgroup's range), with pages of
+    32 or 128 tokens (a step spans four pages or one)."""
+    g = torch.Generator().manual_seed(21 + bs)
+    hist = [5000, 333, 4097] + torch.randint(200, 3000, (3,), generator=g).tolist()
+    case = decode_case(hist, [4, 1, 3, 2, 4, 1], bs=bs, seed=22, sink=2 * bs, recent=256, staging=8192)
+    L = case.layer
+    q, k, v = case.rotated()
+    stage = L.stage()
+    want = oatt.paged_attention_ref(q, k, v, L.k_cache, L.v_cache, case.bt, case.qsl, case.seqs, L.scale, stage)
+    dstage = tuple(t.to(device) for t in stage)
+    p = decode.plan(q.to(device), k.to(device), v.to(device), L.k_cache.to(device), L.v_cache.to(device),
+                    case.bt.to(device), case.qsl, case.seqs, L.scale, dstage, tiles_per_split=tiles_per_split)
+    got = p.launch()
+    torch.cuda.synchronize()
+    got = got.cpu()
+    err = (got - want).abs().max().item()
+    assert torch.isfinite(got).all()
+    assert err <= REL_TOL * want.abs().max().item(), f"max err {err:.3e}"
