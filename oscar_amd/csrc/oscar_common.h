@@ -36,6 +36,32 @@ enum Status : int {
   kErrUnsupportedGeometry = -5,
 };
 
+// Division of n in [0, 2^31) by a divisor d in [1, 2^31) fixed at launch, as
+// a multiply-high, an add and a shift (Granlund and Montgomery, "Division by
+// invariant integers using multiplication", PLDI 1994, theorem 4.2): with
+// 2^(l-1) < d <= 2^l and M = floor(2^(32+l) / d) + 1 = 2^32 + m (m < 2^32),
+// floor(n / d) = floor(M n / 2^(32+l)) = (n + mulhi(m, n)) >> l, and the sum
+// stays below 2^32 because mulhi(m, n) < n < 2^31.
+struct FastDiv {
+  uint32_t d, m;
+  int32_t l;
+};
+
+inline FastDiv make_fast_div(uint32_t d) {      // host side, d >= 1
+  int32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  const uint64_t m = ((((uint64_t)1 << l) - d) << 32) / d + 1;
+  return FastDiv{d, (uint32_t)m, l};
+}
+
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv& f) {
+  return (__umulhi(f.m, n) + n) >> f.l;
+}
+
+__device__ __forceinline__ uint32_t fast_mod(uint32_t n, const FastDiv& f) {
+  return n - fast_div(n, f) * f.d;
+}
+
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
   _Float16 h = (_Float16)x;            // v_cvt_f16_f32, round-to-nearest-even
   return __builtin_bit_cast(uint16_t, h);

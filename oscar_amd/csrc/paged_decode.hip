@@ -94,6 +94,8 @@ struct DecodeArgs {
   const uint8_t* v_cache;
   int64_t k_page, k_tok, k_head, v_page, v_tok, v_head;
   int32_t block_size;
+  FastDiv bs_div;               // block_size
+  FastDiv rows_div;             // stage_rows (1 without an arena)
   int64_t num_pages;
   const int32_t* block_table;
   int64_t bt_stride;
@@ -204,7 +206,7 @@ __device__ __forceinline__ StepLoad load_step(const DecodeArgs& a, const int (&p
   const int page = pg[w];
   const bool tile_ok = p0 < prefix && page >= 0;
   const int pgc = tile_ok ? page : 0;
-  const int prow0 = p0 % a.block_size;
+  const int prow0 = (int)fast_mod((uint32_t)p0, a.bs_div);
   const uint8_t* kbase = a.k_cache + (int64_t)pgc * a.k_page + (int64_t)kvh * a.k_head;
   const uint8_t* vbase = a.v_cache + (int64_t)pgc * a.v_page + (int64_t)kvh * a.v_head;
   const int trow = (tile_ok && p0 + t < prefix) ? prow0 + t : 0;
@@ -230,7 +232,8 @@ __device__ __forceinline__ StepLoad load_step(const DecodeArgs& a, const int (&p
     const int pj = j == 0 ? pg[0] : (j == 1 ? pg[1] : (j == 2 ? pg[2] : pg[3]));
     const int pos = tbase + tk;
     const bool ok = arena && pj >= 0 && pos < prefix;
-    const int64_t* op = ok ? a.owner + (int64_t)(pj % a.stage_rows) * a.block_size + pos % a.block_size
+    const int64_t* op = ok ? a.owner + (int64_t)fast_mod((uint32_t)pj, a.rows_div) * a.block_size +
+                                 fast_mod((uint32_t)pos, a.bs_div)
                            : reinterpret_cast<const int64_t*>(ks);
     // Owner tags are pages (< 2^31) or -1: the low word identifies them
     // (little-endian int64).
@@ -264,7 +267,8 @@ __device__ __forceinline__ void k_operands(uint32_t w, uint32_t ones, half8 (&ka
 // Index of the staged operand image of the tile whose first row is prow0 on
 // `page` (the arena seat row is page % rows).
 __device__ __forceinline__ int64_t image_index(const DecodeArgs& a, int page, int prow0, int kvh) {
-  return ((int64_t)(page % a.stage_rows) * (a.block_size / kTile) + prow0 / kTile) * a.num_kv_heads + kvh;
+  return ((int64_t)fast_mod((uint32_t)page, a.rows_div) * (a.block_size / kTile) + prow0 / kTile) * a.num_kv_heads +
+         kvh;
 }
 // The step's own new tokens of one item, exact fp32: row (token j, head h)
 // against new keys 0 .. j, written as a partial like a history split's.
@@ -395,18 +399,10 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   const int nst = (steps - 1 - split) / nsplit + 1;     // steps split + nsplit k, k < nst (<= 64)
   const bool arena = a.stage_rows > 0;
 
-  // ---- requests before any wait: the pages of the workgroup's tiles (lane k
-  // of pgv[j]: tile j of step k), the query features, then the first step ----
-  int pgv[kWaves];
-#pragma unroll
-  for (int j = 0; j < kWaves; ++j) {
-    pgv[j] = -1;
-    const int64_t tok0 = (int64_t)(split + nsplit * lane) * kStepTok + kTile * j;
-    if (lane < nst && tok0 < prefix) {
-      const int64_t pidx = tok0 / a.block_size;
-      if (pidx < a.bt_cols) pgv[j] = a.block_table[(int64_t)it.req * a.bt_stride + pidx];
-    }
-  }
+  // ---- requests before any wait: the query features, then the pages of the
+  // workgroup's tiles (lane k of pgv[j]: tile j of step k), then the first
+  // step.  The page reads are unconditional (an unused lane reads column 0)
+  // so that the query and page loads issue back to back. ----
   const int r8 = tid >> 3, c8 = tid & 7;
   floatx4 x[8];
   {
@@ -418,6 +414,18 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
 #pragma unroll
     for (int k = 0; k < 8; ++k) x[k] = src[k];
   }
+  __builtin_amdgcn_sched_barrier(0);      // the query loads go out first
+  int pgv[kWaves];
+  const int32_t* bt_row = a.block_table + (int64_t)it.req * a.bt_stride;
+#pragma unroll
+  for (int j = 0; j < kWaves; ++j) {
+    // token offsets stay below 2^31: (split + nsplit * lane) * 128 < 1024 * 64 * 128
+    const uint32_t tok0 = (uint32_t)(split + nsplit * lane) * kStepTok + kTile * j;
+    const uint32_t pidx = fast_div(tok0, a.bs_div);
+    const bool ok = lane < nst && (int)tok0 < prefix && (int)pidx < a.bt_cols;
+    const int p = bt_row[ok ? pidx : 0];
+    pgv[j] = ok ? p : -1;
+  }
   auto step_pages = [&](int k, int (&pg)[kWaves]) {
 #pragma unroll
     for (int j = 0; j < kWaves; ++j) {
@@ -427,10 +435,10 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   };
   int pg[kWaves];
   step_pages(0, pg);
-  StepLoad cur = load_step(a, pg, split * kStepTok, prefix, kvh, w, lane);
-  // Touch the pages of this wave's later tiles in both caches now (lane k:
-  // step k), so that their address translations overlap the first step
-  // instead of each step's own loads.
+  // Touch the pages of this wave's later tiles in both caches (lane k: step
+  // k), so that their address translations overlap the first step instead of
+  // each step's own loads.  The words are consumed (below) where the first
+  // step's loads, issued after them, are needed anyway.
   uint32_t touched;
   {
     const int pk = pick4(pgv[0], pgv[1], pgv[2], pgv[3], w);
@@ -438,6 +446,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
     touched = *reinterpret_cast<const uint32_t*>(a.k_cache + pgk * a.k_page) ^
               *reinterpret_cast<const uint32_t*>(a.v_cache + pgk * a.v_page);
   }
+  StepLoad cur = load_step(a, pg, split * kStepTok, prefix, kvh, w, lane);
 
   // ---- Q^T operand into LDS (permuted K dimension, fp16) and row sums ----
   // Thread: row r8, features 32 * c8 .. +31, which are exactly the four
@@ -467,6 +476,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
     if (c8 == 0) S.qsum[r8] = (rt * kRows + r8 < rows) ? qs : 0.f;
   }
   lds_barrier();
+  asm volatile("" ::"v"(touched));
 
   floatx16 acc[2] = {floatx16{}, floatx16{}};   // O^T of features 64w .. 64w + 63 (2 blocks of 32)
   float m_run = -__builtin_inff();
@@ -559,7 +569,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
         }
       } else {
         const u32x4* img = reinterpret_cast<const u32x4*>(
-            a.kimg + image_index(a, pgw, p0 % a.block_size, kvh) * kImgHalfs);
+            a.kimg + image_index(a, pgw, (int)fast_mod((uint32_t)p0, a.bs_div), kvh) * kImgHalfs);
         u32x4 im[16];
 #pragma unroll
         for (int m = 0; m < 16; ++m) im[m] = img[m * 64 + lane];
@@ -585,7 +595,8 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
         const uint32_t wmj = j == 0 ? wm0 : (j == 1 ? wm1 : (j == 2 ? wm2 : wm3));
         if (wmj != 0u) {
           const half8* vimg = reinterpret_cast<const half8*>(
-              a.vimg + image_index(a, pgs[j], (tbase + kTile * j) % a.block_size, kvh) * kImgHalfs);
+              a.vimg + image_index(a, pgs[j], (int)fast_mod((uint32_t)(tbase + kTile * j), a.bs_div), kvh) *
+                           kImgHalfs);
 #pragma unroll
           for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -760,8 +771,6 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
     part[kPartO + lane] = m_run;
     part[kPartO + kRows + lane] = lt;
   }
-  // (a condition that never holds: keeps the page-touching loads alive)
-  if (a.stage_rows < 0 && touched == 0x5EEDu) part[kPartO] = 0.f;
 }
 
 // One 256-thread block per (output row, quarter of the features) of an item.
@@ -963,7 +972,7 @@ int oscar_paged_decode(const float* q_rot, const float* k_new, const float* v_ne
     if (nq < 0 || nq > max_query_len || seq_lens[i] < nq || (int64_t)(seq_lens[i] - nq) > max_history)
       return kErrInvalidArgument;
   }
-  if (max_history > 0 && !block_table) return kErrInvalidArgument;
+  if (max_history > 0 && (!block_table || block_table_cols <= 0)) return kErrInvalidArgument;
   if (stage_rows > 0 && (!stage_owner || !stage_k_image || !stage_v_image)) return kErrInvalidArgument;
   if (stage_rows > 0 && ((reinterpret_cast<uintptr_t>(stage_k_image) & 15) ||
                          (reinterpret_cast<uintptr_t>(stage_v_image) & 15)))
@@ -994,6 +1003,8 @@ int oscar_paged_decode(const float* q_rot, const float* k_new, const float* v_ne
   a.v_tok = v_stride_token;
   a.v_head = v_stride_head;
   a.block_size = block_size;
+  a.bs_div = make_fast_div((uint32_t)block_size);
+  a.rows_div = make_fast_div(stage_rows > 0 ? (uint32_t)stage_rows : 1u);
   a.num_pages = num_pages;
   a.bt_stride = block_table_stride;
   a.bt_cols = block_table_cols;
