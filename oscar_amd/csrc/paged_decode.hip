@@ -62,8 +62,6 @@ constexpr int kStepTok = kWaves * kTile;  // history tokens per step: one tile p
 constexpr int kMaxFresh = 16;
 constexpr int kPRow = 40;               // halves per P' row: 32 token slots + pad (16-byte rows)
 constexpr int kVtRow = 10;              // dwords per V code byte row: 8 groups of 4 tokens + pad
-constexpr int kTRow = 68;               // floats per staged output row: 64 features + pad
-constexpr int kTFloats = kRows * kTRow;
 constexpr int kImgHalfs = 16 * 64 * 8;  // one staged operand image: 16 blocks x 64 lanes x 8
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 4.f;            // log2 headroom before a running max is raised
@@ -509,6 +507,16 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
     const int pgw = pick4(pgs[0], pgs[1], pgs[2], pgs[3], w);
     const int p0 = tbase + kTile * w;
     const int nvalid = pgw >= 0 ? min(kTile, max(prefix - p0, 0)) : 0;
+    // A tile with window tokens reads the first half of their K operand
+    // image now, a phase before the score pass uses it (the second half goes
+    // out at the start of that pass).
+    const u32x4* img = reinterpret_cast<const u32x4*>(
+        a.kimg + image_index(a, wmw != 0u ? pgw : 0, (int)fast_mod((uint32_t)p0, a.bs_div), kvh) * kImgHalfs);
+    u32x4 im[16];
+    if (wmw != 0u) {
+#pragma unroll
+      for (int m = 0; m < 8; ++m) im[m] = img[m * 64 + lane];
+    }
 
     // ---- own tile: token parameters and byte-transposed V codes ----
     bool big;
@@ -568,11 +576,8 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
           qk_pair(j, ka[0], ka[1]);
         }
       } else {
-        const u32x4* img = reinterpret_cast<const u32x4*>(
-            a.kimg + image_index(a, pgw, (int)fast_mod((uint32_t)p0, a.bs_div), kvh) * kImgHalfs);
-        u32x4 im[16];
 #pragma unroll
-        for (int m = 0; m < 16; ++m) im[m] = img[m * 64 + lane];
+        for (int m = 8; m < 16; ++m) im[m] = img[m * 64 + lane];
         const bool wl = (wmw >> col) & 1u;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -724,11 +729,13 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   run_step(cur, k, pg);
 
   // ---- row sums over both lane halves and the four waves, then the partial ----
+  // The sums go through the Q^T area, which no wave reads after the last
+  // step's scores (every wave has passed that step's barriers by now).
   l_run += shfl_xor_f32(l_run, 32);
   z_run += shfl_xor_f32(z_run, 32);
   ps_run += shfl_xor_f32(ps_run, 32);
-  lds_barrier();                                  // the step buffers are free from here on
-  float* red = reinterpret_cast<float*>(&S.buf[0]);
+  float* red = reinterpret_cast<float*>(S.q);
+  static_assert(sizeof(S.q) >= kWaves * 3 * kRows * sizeof(float), "row sums fit the Q^T area");
   if (g == 0) {
     red[(w * 3 + 0) * kRows + col] = l_run;
     red[(w * 3 + 1) * kRows + col] = z_run;
@@ -744,28 +751,20 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   }
   // sum_t p (c vs + vz) = 4 * acc - 4 * sum_t P' + sum_t p vz
   const float off = zt - 4.f * pt;
-  // Register 4jq + i of block b is local feature 16jq + 8g + 4(i >> 1) + 2b +
-  // (i & 1) of row col: staged as [row][64 + 4 pad] fp32.
-  float* tbuf = red + kWaves * 3 * kRows + w * kTFloats;
-#pragma unroll
-  for (int jq = 0; jq < 4; ++jq) {
-    float* d = tbuf + col * kTRow + 16 * jq + 8 * g;
-    *reinterpret_cast<floatx4*>(d) =
-        floatx4{fmaf(4.f, acc[0][4 * jq], off), fmaf(4.f, acc[0][4 * jq + 1], off),
-                fmaf(4.f, acc[1][4 * jq], off), fmaf(4.f, acc[1][4 * jq + 1], off)};
-    *reinterpret_cast<floatx4*>(d + 4) =
-        floatx4{fmaf(4.f, acc[0][4 * jq + 2], off), fmaf(4.f, acc[0][4 * jq + 3], off),
-                fmaf(4.f, acc[1][4 * jq + 2], off), fmaf(4.f, acc[1][4 * jq + 3], off)};
-  }
-  wave_sync_lds();
+  // Registers 4jq + 2h, 4jq + 2h + 1 of blocks 0 and 1 are local features
+  // 16jq + 8g + 4h + 0 .. 3 of row col: stored straight from the registers.
   const int nrow = min(kRows, rows - rt * kRows);
   float* part = a.ws + item_index(a, item, split, rt) * kPartialFloats;
+  if (col < nrow) {
+    float* dst = part + col * kHeadDim + 64 * w + 8 * g;
 #pragma unroll
-  for (int s4 = 0; s4 < kRows / 4; ++s4) {
-    const int row = 4 * s4 + (lane >> 4);
-    if (row < nrow)
-      *reinterpret_cast<floatx4*>(part + row * kHeadDim + 64 * w + 4 * (lane & 15)) =
-          *reinterpret_cast<const floatx4*>(tbuf + row * kTRow + 4 * (lane & 15));
+    for (int jq = 0; jq < 4; ++jq) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        *reinterpret_cast<floatx4*>(dst + 16 * jq + 4 * h) =
+            floatx4{fmaf(4.f, acc[0][4 * jq + 2 * h], off), fmaf(4.f, acc[0][4 * jq + 2 * h + 1], off),
+                    fmaf(4.f, acc[1][4 * jq + 2 * h], off), fmaf(4.f, acc[1][4 * jq + 2 * h + 1], off)};
+    }
   }
   if (w == 0 && lane < nrow) {
     part[kPartO + lane] = m_run;
