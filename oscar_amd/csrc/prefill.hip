@@ -35,6 +35,7 @@ constexpr int kVs = kBlk + 4;         // halfs per V feature row in LDS (72 B: 8
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.f;          // log2 headroom before a running max is raised
+constexpr float kVsMax = 240.f;       // p vs stays below 2^kLazy * 240 < 65504 (fp16) under the lazy max
 
 struct PrefillArgs {
   const float* q;        // [N][Hq][D]
@@ -46,6 +47,8 @@ struct PrefillArgs {
   const uint8_t* v_cache;
   int64_t k_page, k_tok, k_head, v_page, v_tok, v_head;
   int32_t block_size;
+  FastDiv bs_div;        // block_size
+  FastDiv rows_div;      // stage_rows (1 without an arena)
   int64_t num_pages;
   const int32_t* bt;     // one request's block-table row
   int32_t bt_cols;
@@ -61,8 +64,11 @@ struct PrefillArgs {
 // Two key blocks of fp16 tiles: block k is computed from one while block
 // k + 1 is written into the other.
 struct PrefillLds {
-  _Float16 kh[2][kBlk * kKs];           // K token-major
-  _Float16 vt[2][kHeadDim * kVs];       // V feature-major
+  _Float16 kh[2][kBlk * kKs];           // K operand, token-major (features permuted, see below)
+  _Float16 vt[2][kHeadDim * kVs];       // V operand, feature-major
+  float kpar[2][2][kBlk];               // per key: score = ta * (K'.q) + tb * sum(q)   [ta | tb]
+  float vpar[2][2][kBlk];               // per key: v = vs * V' + vz                    [vs | vz]
+  uint32_t big[2][4];                   // a key of the block has vs above kVsMax
   _Float16 q[kWaves][16 * 2 * kRowsPerWave * 8];   // Q^T operands [wave][m][g][row][8]
 };
 constexpr size_t kPrefillLds = sizeof(PrefillLds);
@@ -121,10 +127,14 @@ struct NewLoad {
   floatx4 v[8];
 };
 
+// Page of the block at key k0 (uniform).  Read through the scalar cache, so
+// that waiting for it never waits for the vector loads in flight.
 __device__ __forceinline__ int32_t block_page(const PrefillArgs& a, int64_t k0) {
-  const int64_t pidx = k0 / a.block_size;
-  const int32_t p = (k0 < a.cached && pidx < a.bt_cols) ? a.bt[pidx] : -1;
-  return p;
+  if (k0 >= a.cached) return -1;
+  const uint32_t pidx = fast_div((uint32_t)k0, a.bs_div);       // key positions stay below 2^31
+  if ((int64_t)pidx >= a.bt_cols) return -1;
+  typedef __attribute__((address_space(4))) const int32_t const_i32;
+  return ((const const_i32*)a.bt)[__builtin_amdgcn_readfirstlane(pidx)];
 }
 
 __device__ __forceinline__ HistLoad load_hist(const PrefillArgs& a, int64_t k0, int32_t page, int kvh, int ktt,
@@ -137,10 +147,11 @@ __device__ __forceinline__ HistLoad load_hist(const PrefillArgs& a, int64_t k0, 
   // Owner tags are pages (< 2^31) or -1: the low word of the little-endian
   // int64 identifies them.  Without an arena the K slot's meta stands in.
   const int32_t* opage = a.stage_rows > 0 ? reinterpret_cast<const int32_t*>(
-                                                a.owner + (pg % a.stage_rows) * a.block_size)
+                                                a.owner + (int64_t)fast_mod((uint32_t)pg, a.rows_div) *
+                                                              a.block_size)
                                           : reinterpret_cast<const int32_t*>(kpage);
   const int ostride = a.stage_rows > 0 ? 2 : 0;
-  const int prow0 = (int)(k0 % a.block_size);
+  const int prow0 = (int)fast_mod((uint32_t)k0, a.bs_div);
   const uint32_t ktok = (uint32_t)a.k_tok, vtok = (uint32_t)a.v_tok;
   {
     const int row = prow0 + ktt;
@@ -180,16 +191,33 @@ __device__ __forceinline__ NewLoad load_new(const PrefillArgs& a, int64_t k0, in
   return L;
 }
 
-__device__ __forceinline__ void store_tiles(const float (&kv)[32], const float (&vv)[4][8], int ktt, int kfg,
-                                            int vtg, int vfg, _Float16* kh, _Float16* vt) {
+// fp16 pair (1 + c/4) of the codes at bits [sh, sh + 2) and [sh + 16, sh + 18)
+// of w (exact: 1, 1.25, 1.5, 1.75).
+__device__ __forceinline__ uint32_t magic_pair(uint32_t w, int sh) {
+  const uint32_t x = sh < 8 ? (w << (8 - sh)) : (w >> (sh - 8));
+  return (x & 0x03000300u) | 0x3C003C00u;
+}
+
+// K tile rows hold each 16-feature group in the order 0, 8, 1, 9, .., 7, 15
+// (position p is feature (p >> 1) + 8 (p & 1)), so that one shift and mask of
+// a code dword yields a pair; the Q^T operand uses the same order.
+__device__ __forceinline__ int k_feature(int p) { return (p >> 1) + 8 * (p & 1); }
+
+// A thread's 32 K values (features 32 kfg .. +31, natural order) into its
+// token's row in the permuted order.
+__device__ __forceinline__ void store_k_values(const float (&kv)[32], int ktt, int kfg, _Float16* kh) {
   half8* dst = reinterpret_cast<half8*>(kh + ktt * kKs + 32 * kfg);
 #pragma unroll
   for (int q8 = 0; q8 < 4; ++q8) {
     half8 x;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = to_h(kv[8 * q8 + e]);
+    for (int e = 0; e < 8; ++e) x[e] = to_h(kv[16 * (q8 >> 1) + k_feature(8 * (q8 & 1) + e)]);
     dst[q8] = x;
   }
+}
+
+// A thread's V values vv[u][w] (feature 4 vfg + u, token 8 vtg + w).
+__device__ __forceinline__ void store_v_values(const float (&vv)[4][8], int vtg, int vfg, _Float16* vt) {
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     half4 lo, hi;
@@ -204,61 +232,112 @@ __device__ __forceinline__ void store_tiles(const float (&kv)[32], const float (
   }
 }
 
-// History tiles: c * s + z in fp32, rounded once to fp16; tokens the staging
-// arena owns are reloaded from it (rare: the sink / recent window).  Keys
-// past C or on an invalid page become whatever the loads held: the consumer
-// masks them.
+// History tiles as code operands: K' = V' = 1 + c/4 (exact in fp16) with the
+// token's scale and zero moved into per-key parameters: k = 4s K' + (z - 4s),
+// so a score is ta (K'.q) + tb sum(q) with ta = 4 s_k, tb = z_k - 4 s_k (times
+// the softmax scale), and v = vs V' + vz with vs = 4 s_v, vz = z_v - 4 s_v.
+// Tokens the staging arena owns (rare: the sink / recent window) keep their
+// FP32 values (rounded to fp16) with ta = scale, tb = 0, vs = 1, vz = 0.  Keys
+// past C or on an unmapped page get all-zero parameters (an unmapped page
+// reads as zeros; keys past C are masked by the consumer).
 __device__ __forceinline__ void store_hist(const PrefillArgs& a, const HistLoad& L, int64_t k0, int32_t page,
                                            int kvh, int ktt, int kfg, int vtg, int vfg, _Float16* kh,
-                                           _Float16* vt) {
-  const bool arena = a.stage_rows > 0 && page >= 0 && page < a.num_pages;
-  const int64_t seat0 = arena ? (int64_t)(page % a.stage_rows) * a.block_size : 0;
-  const int prow0 = (int)(k0 % a.block_size);
-  float kv[32];
-  float vv[4][8];
+                                           _Float16* vt, float (&kpar)[2][kBlk], float (&vpar)[2][kBlk],
+                                           uint32_t* big) {
+  const bool page_ok = page >= 0 && page < a.num_pages;
+  const bool arena = a.stage_rows > 0 && page_ok;
+  const int64_t seat0 = arena ? (int64_t)fast_mod((uint32_t)page, a.rows_div) * a.block_size : 0;
+  const int prow0 = (int)fast_mod((uint32_t)k0, a.bs_div);
+  const int64_t C = a.cached;
   {
-    const float sc = f16_bits_to_f32(L.k[2]), zr = f16_bits_to_f32(L.k[2] >> 16);
+    const bool live = page_ok && k0 + ktt < C;
+    const bool win = arena && live && (int32_t)L.k[3] == page;
+    if (!win) {
+      half8* dst = reinterpret_cast<half8*>(kh + ktt * kKs + 32 * kfg);
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      kv[u] = (float)((L.k[0] >> (2 * u)) & 3u) * sc + zr;
-      kv[16 + u] = (float)((L.k[1] >> (2 * u)) & 3u) * sc + zr;
-    }
-    if (arena && (int32_t)L.k[3] == page) {
+      for (int q8 = 0; q8 < 4; ++q8) {
+        const uint32_t w = L.k[q8 >> 1];
+        const int j0 = 4 * (q8 & 1);
+        dst[q8] = __builtin_bit_cast(half8, u32x4{magic_pair(w, 2 * j0), magic_pair(w, 2 * j0 + 2),
+                                                  magic_pair(w, 2 * j0 + 4), magic_pair(w, 2 * j0 + 6)});
+      }
+    } else {
       const floatx4* src = reinterpret_cast<const floatx4*>(
           a.stage_k + ((seat0 + prow0 + ktt) * a.num_kv_heads + kvh) * kHeadDim + 32 * kfg);
+      float kv[32];
 #pragma unroll
       for (int q4 = 0; q4 < 8; ++q4) {
         const floatx4 x = src[q4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) kv[4 * q4 + e] = x[e];
       }
+      store_k_values(kv, ktt, kfg, kh);
+    }
+    if (kfg == 0) {
+      const float sc = f16_bits_to_f32(L.k[2]), zr = f16_bits_to_f32(L.k[2] >> 16);
+      kpar[0][ktt] = win ? a.scale_log2 : (live ? 4.f * sc * a.scale_log2 : 0.f);
+      kpar[1][ktt] = (win || !live) ? 0.f : (zr - 4.f * sc) * a.scale_log2;
     }
   }
+  {
+    uint32_t winmask = 0u, livemask = 0u;
 #pragma unroll
-  for (int w = 0; w < 8; ++w) {
-    const float sc = f16_bits_to_f32(L.vm[w]), zr = f16_bits_to_f32(L.vm[w] >> 16);
+    for (int w = 0; w < 8; ++w) {
+      const bool live = page_ok && k0 + 8 * vtg + w < C;
+      livemask |= live ? 1u << w : 0u;
+      winmask |= (arena && live && (int32_t)L.vo[w] == page) ? 1u << w : 0u;
+    }
+    if (winmask == 0u) {
+      // Code bytes of tokens 8 vtg + 0..3 and + 4..7; per feature u the codes
+      // at bits 2u of each byte become fp16 pairs (1 + c/4) of two tokens.
+      const uint32_t b0 = L.vb[0] | (L.vb[1] << 8) | (L.vb[2] << 16) | (L.vb[3] << 24);
+      const uint32_t b1 = L.vb[4] | (L.vb[5] << 8) | (L.vb[6] << 16) | (L.vb[7] << 24);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) vv[u][w] = (float)((L.vb[w] >> (2 * u)) & 3u) * sc + zr;
-    if (arena && (int32_t)L.vo[w] == page) {
-      const floatx4 y = *reinterpret_cast<const floatx4*>(
-          a.stage_v + ((seat0 + prow0 + 8 * vtg + w) * a.num_kv_heads + kvh) * kHeadDim + 4 * vfg);
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t y0 = ((b0 >> (2 * u)) & 0x03030303u) | 0x3C3C3C3Cu;
+        const uint32_t y1 = ((b1 >> (2 * u)) & 0x03030303u) | 0x3C3C3C3Cu;
+        // bytes {0, y.b0, 0, y.b1} and {0, y.b2, 0, y.b3}
+        const u32x2 lo{__builtin_amdgcn_perm(0u, y0, 0x010C000Cu), __builtin_amdgcn_perm(0u, y0, 0x030C020Cu)};
+        const u32x2 hi{__builtin_amdgcn_perm(0u, y1, 0x010C000Cu), __builtin_amdgcn_perm(0u, y1, 0x030C020Cu)};
+        u32x2* d = reinterpret_cast<u32x2*>(vt + (4 * vfg + u) * kVs + 8 * vtg);
+        d[0] = lo;
+        d[1] = hi;
+      }
+    } else {
+      float vv[4][8];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) vv[u][w] = y[u];
+      for (int w = 0; w < 8; ++w) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) vv[u][w] = 1.f + 0.25f * (float)((L.vb[w] >> (2 * u)) & 3u);
+        if ((winmask >> w) & 1u) {
+          const floatx4 y = *reinterpret_cast<const floatx4*>(
+              a.stage_v + ((seat0 + prow0 + 8 * vtg + w) * a.num_kv_heads + kvh) * kHeadDim + 4 * vfg);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) vv[u][w] = y[u];
+        }
+      }
+      store_v_values(vv, vtg, vfg, vt);
+    }
+    if (vfg == 0) {
+      bool bg = false;
+#pragma unroll
+      for (int w = 0; w < 8; ++w) {
+        const float sc = f16_bits_to_f32(L.vm[w]), zr = f16_bits_to_f32(L.vm[w] >> 16);
+        const bool live = (livemask >> w) & 1u, win = (winmask >> w) & 1u;
+        vpar[0][8 * vtg + w] = win ? 1.f : (live ? 4.f * sc : 0.f);
+        vpar[1][8 * vtg + w] = (win || !live) ? 0.f : zr - 4.f * sc;
+        bg = bg || (live && !win && 4.f * sc > kVsMax);
+      }
+      big[vtg] = bg ? 1u : 0u;
     }
   }
-  if (!(page >= 0 && page < a.num_pages)) {     // an unmapped page reads as zeros
-#pragma unroll
-    for (int u = 0; u < 32; ++u) kv[u] = 0.f;
-#pragma unroll
-    for (int w = 0; w < 8; ++w)
-#pragma unroll
-      for (int u = 0; u < 4; ++u) vv[u][w] = 0.f;
-  }
-  store_tiles(kv, vv, ktt, kfg, vtg, vfg, kh, vt);
 }
 
-__device__ __forceinline__ void store_new(const NewLoad& L, int ktt, int kfg, int vtg, int vfg, _Float16* kh,
-                                          _Float16* vt) {
+// New-token tiles: the fp32 values rounded to fp16, ta = scale, tb = 0,
+// vs = 1, vz = 0.
+__device__ __forceinline__ void store_new(const PrefillArgs& a, const NewLoad& L, int ktt, int kfg, int vtg, int vfg,
+                                          _Float16* kh, _Float16* vt, float (&kpar)[2][kBlk],
+                                          float (&vpar)[2][kBlk], uint32_t* big) {
   float kv[32];
   float vv[4][8];
 #pragma unroll
@@ -269,7 +348,20 @@ __device__ __forceinline__ void store_new(const NewLoad& L, int ktt, int kfg, in
   for (int w = 0; w < 8; ++w)
 #pragma unroll
     for (int u = 0; u < 4; ++u) vv[u][w] = L.v[w][u];
-  store_tiles(kv, vv, ktt, kfg, vtg, vfg, kh, vt);
+  store_k_values(kv, ktt, kfg, kh);
+  store_v_values(vv, vtg, vfg, vt);
+  if (kfg == 0) {
+    kpar[0][ktt] = a.scale_log2;
+    kpar[1][ktt] = 0.f;
+  }
+  if (vfg == 0) {
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      vpar[0][8 * vtg + w] = 1.f;
+      vpar[1][8 * vtg + w] = 0.f;
+    }
+    big[vtg] = 0u;
+  }
 }
 
 // 8 wavefronts: waves 0-3 compute (32 rows each), waves 4-7 produce the
@@ -299,34 +391,52 @@ __global__ __launch_bounds__(512, 1) void prefill_kernel(PrefillArgs a) {
     const int ktt = ptid >> 3, kfg = ptid & 7;       // K: token ktt, features 32*kfg .. +31
     const int vtg = ptid >> 6, vfg = ptid & 63;      // V: tokens 8*vtg .. +7, features 4*vfg .. +3
     // History pass: loads of block i + 2 out while block i + 1's are turned
-    // into tiles; then the same for the new-token pass.
+    // into tiles; then the same for the new-token pass.  The loop is unrolled
+    // twice so that the two load sets alternate in place: a load never lands
+    // in registers that still have to be copied, and each wait counts one
+    // block's loads.
     const int64_t nh = plan.n_hist;
-    int32_t pg_a = block_page(a, 0), pg_b = block_page(a, kBlk);
     int64_t i = 0;
     if (nh > 0) {
+      int32_t pg_a = block_page(a, 0), pg_b = block_page(a, kBlk);
       HistLoad La = load_hist(a, 0, pg_a, kvh, ktt, kfg, vtg, vfg);
       HistLoad Lb = load_hist(a, kBlk, pg_b, kvh, ktt, kfg, vtg, vfg);
       int32_t pg_c = block_page(a, 2 * kBlk);
+      // top of the loop: La holds block i (page pg_a), Lb block i + 1 (pg_b),
+      // pg_c is block i + 2's page
 #pragma unroll 1
-      for (; i < nh; ++i) {
-        store_hist(a, La, i * kBlk, pg_a, kvh, ktt, kfg, vtg, vfg, S.kh[i & 1], S.vt[i & 1]);
-        La = Lb;
-        pg_a = pg_b;
-        Lb = load_hist(a, (i + 2) * kBlk, pg_c, kvh, ktt, kfg, vtg, vfg);
-        pg_b = pg_c;
-        pg_c = block_page(a, (i + 3) * kBlk);
+      for (;;) {
+        store_hist(a, La, i * kBlk, pg_a, kvh, ktt, kfg, vtg, vfg, S.kh[i & 1], S.vt[i & 1], S.kpar[i & 1],
+                   S.vpar[i & 1], S.big[i & 1]);
+        const int32_t pg_d = block_page(a, (i + 3) * kBlk);
+        La = load_hist(a, (i + 2) * kBlk, pg_c, kvh, ktt, kfg, vtg, vfg);
+        pg_a = pg_c;
         lds_barrier();        // tiles of block i ready / block i - 1 consumed
+        if (++i == nh) break;
+        store_hist(a, Lb, i * kBlk, pg_b, kvh, ktt, kfg, vtg, vfg, S.kh[i & 1], S.vt[i & 1], S.kpar[i & 1],
+                   S.vpar[i & 1], S.big[i & 1]);
+        pg_c = block_page(a, (i + 3) * kBlk);
+        Lb = load_hist(a, (i + 2) * kBlk, pg_d, kvh, ktt, kfg, vtg, vfg);
+        pg_b = pg_d;
+        lds_barrier();
+        if (++i == nh) break;
       }
     }
     if (plan.n_new > 0) {
       NewLoad La = load_new(a, plan.new0, kvh, ktt, kfg, vtg, vfg);
       NewLoad Lb = load_new(a, plan.new0 + kBlk, kvh, ktt, kfg, vtg, vfg);
 #pragma unroll 1
-      for (; i < nblk; ++i) {
-        store_new(La, ktt, kfg, vtg, vfg, S.kh[i & 1], S.vt[i & 1]);
-        La = Lb;
+      for (;;) {
+        store_new(a, La, ktt, kfg, vtg, vfg, S.kh[i & 1], S.vt[i & 1], S.kpar[i & 1], S.vpar[i & 1],
+                  S.big[i & 1]);
+        La = load_new(a, block_k0(i) + 2 * kBlk, kvh, ktt, kfg, vtg, vfg);
+        lds_barrier();
+        if (++i == nblk) break;
+        store_new(a, Lb, ktt, kfg, vtg, vfg, S.kh[i & 1], S.vt[i & 1], S.kpar[i & 1], S.vpar[i & 1],
+                  S.big[i & 1]);
         Lb = load_new(a, block_k0(i) + 2 * kBlk, kvh, ktt, kfg, vtg, vfg);
         lds_barrier();
+        if (++i == nblk) break;
       }
     }
     lds_barrier();            // the consumers' last block
@@ -340,21 +450,36 @@ __global__ __launch_bounds__(512, 1) void prefill_kernel(PrefillArgs a) {
   const int64_t wave_last = min(wrow0 + kRowsPerWave, rows_total) - 1;
   const int64_t keys_wave = wrow0 < rows_total ? C + wave_last / a.group + 1 : 0;
   const int64_t my_limit = row_ok ? C + row / a.group : -1;   // last visible key
+  // Keys every row of the wave sees (all rows in range): history keys
+  // 0 .. C - 1 in the history pass, C .. C + wrow0 / group in the new pass.
+  const bool wave_full = wrow0 + kRowsPerWave <= rows_total;
+  const int32_t full_hi_new = (int32_t)(C + wrow0 / a.group);
+  auto lo_wave = [&](bool hist) { return hist ? 0 : (int32_t)C; };
+  auto hi_wave = [&](bool hist) {
+    return wave_full ? (hist ? (int32_t)C - 1 : full_hi_new) : (int32_t)-1;
+  };
+  float qsum;
   {
-    // Q^T operands of the wave's rows: lane (row col, half g) holds features
-    // 16m + 8g .. +7 of k-step m.
+    // Q^T operands of the wave's rows in the K tiles' feature order: lane
+    // (row col, half g) holds positions 8g .. 8g + 7 of k-step m, i.e.
+    // features 16m + 4g + {0, 8, 1, 9, 2, 10, 3, 11}.  qsum: the row's sum of
+    // the fp16 values.
     const int64_t j = row_ok ? row / a.group : 0;
     const int h = kvh * a.group + (row_ok ? (int)(row % a.group) : 0);
-    const float* qp = a.q + (j * a.num_heads + h) * kHeadDim + 8 * g;
+    const float* qp = a.q + (j * a.num_heads + h) * kHeadDim + 4 * g;
     _Float16* qdst = S.q[wave] + (g * kRowsPerWave + col) * 8;
+    float qs = 0.f;
 #pragma unroll
     for (int m = 0; m < 16; ++m) {
-      floatx4 x0 = row_ok ? *reinterpret_cast<const floatx4*>(qp + 16 * m) : floatx4{};
-      floatx4 x1 = row_ok ? *reinterpret_cast<const floatx4*>(qp + 16 * m + 4) : floatx4{};
-      *reinterpret_cast<half8*>(qdst + m * 2 * kRowsPerWave * 8) =
-          half8{to_h(x0[0]), to_h(x0[1]), to_h(x0[2]), to_h(x0[3]),
-                to_h(x1[0]), to_h(x1[1]), to_h(x1[2]), to_h(x1[3])};
+      const floatx4 x0 = row_ok ? *reinterpret_cast<const floatx4*>(qp + 16 * m) : floatx4{};
+      const floatx4 x1 = row_ok ? *reinterpret_cast<const floatx4*>(qp + 16 * m + 8) : floatx4{};
+      const half8 v = half8{to_h(x0[0]), to_h(x1[0]), to_h(x0[1]), to_h(x1[1]),
+                            to_h(x0[2]), to_h(x1[2]), to_h(x0[3]), to_h(x1[3])};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qs += (float)v[e];
+      *reinterpret_cast<half8*>(qdst + m * 2 * kRowsPerWave * 8) = v;
     }
+    qsum = qs + shfl_xor_f32(qs, 32);
   }
   wave_sync_lds();
 
@@ -362,7 +487,7 @@ __global__ __launch_bounds__(512, 1) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
   for (int t = 0; t < 8; ++t) acc[t] = floatx16{};
   float m_run = -__builtin_inff();
-  float l_run = 0.f;
+  float l_run = 0.f, z_run = 0.f;     // this lane's keys' sums of p and p vz
 
 #pragma unroll 1
   for (int64_t i = 0; i < nblk; ++i) {
@@ -383,41 +508,71 @@ __global__ __launch_bounds__(512, 1) void prefill_kernel(PrefillArgs a) {
       }
       floatx16 s = s0 + s1;
       // Visible keys of this pass: history keys < C in the history pass, new
-      // keys >= C in the new-token pass, causal for both.
-      const int64_t lo = hist ? 0 : C;
-      const int64_t hi = hist ? min(C - 1, my_limit) : my_limit;
-      float mb = -__builtin_inff();
+      // keys >= C in the new-token pass, causal for both.  A block every row
+      // of the wave sees whole skips the per-key test.
+      const int32_t lo = hist ? 0 : (int32_t)C;
+      const int32_t hi = hist ? (int32_t)min(C - 1, my_limit) : (int32_t)my_limit;
+      const bool whole = (int32_t)k0 >= lo_wave(hist) && (int32_t)k0 + kBlk - 1 <= hi_wave(hist);
+      // key 8 jj + 4g + i of the block is register 4 jj + i
+      const float* kpar0 = S.kpar[i & 1][0] + 4 * g;
+      const float* kpar1 = S.kpar[i & 1][1] + 4 * g;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t kp = k0 + 8 * (r >> 2) + 4 * g + (r & 3);
-        const float x = (kp >= lo && kp <= hi) ? s[r] * a.scale_log2 : -__builtin_inff();
-        s[r] = x;
-        mb = fmaxf(mb, x);
+      for (int jj = 0; jj < 4; ++jj) {
+        const floatx4 ta = *reinterpret_cast<const floatx4*>(kpar0 + 8 * jj);
+        const floatx4 tb = *reinterpret_cast<const floatx4*>(kpar1 + 8 * jj);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[4 * jj + e] = fmaf(ta[e], s[4 * jj + e], tb[e] * qsum);
+      }
+      float mb = -__builtin_inff();
+      if (whole) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mb = fmaxf(mb, s[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int32_t kp = (int32_t)k0 + 8 * (r >> 2) + 4 * g + (r & 3);
+          const float x = (kp >= lo && kp <= hi) ? s[r] : -__builtin_inff();
+          s[r] = x;
+          mb = fmaxf(mb, x);
+        }
       }
       mb = fmaxf(mb, shfl_xor_f32(mb, 32));
       // Lazy running max: raised only when a block exceeds it by more than
-      // 2^kLazy (probabilities stay <= 2^kLazy, exact range for fp16), and the
-      // first raise of a row needs no rescale.
-      const bool need = mb > m_run + kLazy;
+      // 2^kLazy (p vs stays in fp16 range), or by any amount when a key of the
+      // block has vs above kVsMax; the first raise of a row needs no rescale.
+      const uint4 bg4 = *reinterpret_cast<const uint4*>(S.big[i & 1]);
+      const bool eager = (bg4[0] | bg4[1] | bg4[2] | bg4[3]) != 0u;
+      const bool need = mb > m_run + (eager ? 0.f : kLazy);
       const bool resc = need && m_run != -__builtin_inff();
       if (__ballot(resc)) {
         const float alpha = resc ? __builtin_amdgcn_exp2f(m_run - mb) : 1.f;
 #pragma unroll
         for (int t = 0; t < 8; ++t) acc[t] *= alpha;
         l_run *= alpha;
+        z_run *= alpha;
       }
       if (need) m_run = mb;
       // exp2(-inf - m) = 0 needs a finite m: rows that have seen no key yet use 0.
       const float m_use = m_run == -__builtin_inff() ? 0.f : m_run;
-      float psum = 0.f;
+      float psum = 0.f, zsum = 0.f;
       half8 pb[2];
+      const float* vpar0 = S.vpar[i & 1][0] + 4 * g;
+      const float* vpar1 = S.vpar[i & 1][1] + 4 * g;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(s[r] - m_use);
-        psum += p;
-        pb[r >> 3][r & 7] = to_h(p);
+      for (int jj = 0; jj < 4; ++jj) {
+        const floatx4 vs = *reinterpret_cast<const floatx4*>(vpar0 + 8 * jj);
+        const floatx4 vz = *reinterpret_cast<const floatx4*>(vpar1 + 8 * jj);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * jj + e;
+          const float p = __builtin_amdgcn_exp2f(s[r] - m_use);
+          psum += p;
+          zsum = fmaf(p, vz[e], zsum);
+          pb[r >> 3][r & 7] = to_h(p * vs[e]);
+        }
       }
       l_run += psum;
+      z_run += zsum;
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) {
 #pragma unroll
@@ -433,8 +588,9 @@ __global__ __launch_bounds__(512, 1) void prefill_kernel(PrefillArgs a) {
   }
   lds_barrier();              // pairs with the producers' last barrier
 
-  if (!row_ok) return;
   const float l_tot = l_run + shfl_xor_f32(l_run, 32);
+  const float z_tot = z_run + shfl_xor_f32(z_run, 32);
+  if (!row_ok) return;
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   const int64_t j = row / a.group;
   const int h = kvh * a.group + (int)(row % a.group);
@@ -442,7 +598,7 @@ __global__ __launch_bounds__(512, 1) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) op[32 * t + 8 * (r >> 2) + 4 * g + (r & 3)] = acc[t][r] * inv;
+    for (int r = 0; r < 16; ++r) op[32 * t + 8 * (r >> 2) + 4 * g + (r & 3)] = (acc[t][r] + z_tot) * inv;
   }
 }
 
@@ -464,6 +620,9 @@ extern "C" int oscar_prefill_continuation(
       block_size <= 0 || num_pages <= 0 || cached_len < 0 || stage_rows < 0 || block_table_cols < 0)
     return kErrInvalidArgument;
   if (num_new == 0) return kOk;
+  // key positions and rows are handled in 32 bits inside the kernel
+  if (cached_len + num_new >= ((int64_t)1 << 31) || (int64_t)num_new * num_heads >= ((int64_t)1 << 31))
+    return kErrInvalidArgument;
   if (!q_rot || !k_new || !v_new || !k_cache || !v_cache || !out) return kErrInvalidArgument;
   if (cached_len > 0 && (!block_table_row || (cached_len + block_size - 1) / block_size > block_table_cols))
     return kErrInvalidArgument;
@@ -488,6 +647,8 @@ extern "C" int oscar_prefill_continuation(
   a.v_tok = v_stride_token;
   a.v_head = v_stride_head;
   a.block_size = block_size;
+  a.bs_div = make_fast_div((uint32_t)block_size);
+  a.rows_div = make_fast_div(stage_rows > 0 ? (uint32_t)stage_rows : 1u);
   a.num_pages = num_pages;
   a.bt = block_table_row;
   a.bt_cols = block_table_cols;
