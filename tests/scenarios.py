@@ -44,9 +44,11 @@ def metadata(slots, qsl, seqs, bt):
 
 def decode_case(history, q_lens, *, hq=6, hk=1, bs=128, pool_pages=None, seed=0,
                 clip=(0.96, 0.92), sink=128, recent=256, staging=8192, window=True,
-                cache_dtype=torch.int8, identity_pages=False) -> DecodeCase:
+                cache_dtype=torch.int8, identity_pages=False, fill_bytes=False) -> DecodeCase:
     """Requests with the given history lengths write their history in one
-    prefill step, then write q_lens new tokens; returns the decode-step state."""
+    prefill step, then write q_lens new tokens; returns the decode-step state.
+    fill_bytes: the caches start as random bytes (an engine's caches are not
+    cleared), so slots nothing wrote hold arbitrary meta, NaN and inf included."""
     B = len(history)
     need = [(h + n + bs - 1) // bs for h, n in zip(history, q_lens)]
     pool = pool_pages or sum(need)
@@ -61,6 +63,12 @@ def decode_case(history, q_lens, *, hq=6, hk=1, bs=128, pool_pages=None, seed=0,
         off += n
     Rk, Rv = synthetic.rotations(D, seed + 2)
     caches = [torch.zeros(pool, bs, hk, D, dtype=cache_dtype) for _ in range(2)]
+    if fill_bytes:
+        g = torch.Generator().manual_seed(seed + 77)
+        for c in caches:
+            raw = c.view(torch.uint8)
+            raw.copy_(torch.randint(0, 256, raw.shape, generator=g, dtype=torch.uint8))
+            raw.view(-1)[1::7] = 0x7C      # fp16 inf / NaN high bytes scattered over the meta
     layer = OracleLayer(caches[0], caches[1], Rk, Rv, hq, hk, D, D ** -0.5, clip[0], clip[1],
                         sink if window else 0, recent if window else 0, staging if window else 0)
     # Prefill step: every request writes its whole history.
