@@ -9,10 +9,16 @@ whole cache blocks.  Per OSCAR layer the fixed buffers here are
   * its fp16 MFMA operand images (K and V)     rows * bs * 2 * Hk * D * 2
   * the arena's seat-winner scratch            rows * bs * 4
 and, once per device, the split-decode workspace of the largest batch.
+
+The engine seams (``install_runner_hooks``) apply that budget before vLLM
+allocates its caches and print one READY manifest per rank after it did;
+``validate_ready`` checks a server log's manifests.
 """
 from __future__ import annotations
 
 import hashlib
+import json
+from copy import deepcopy
 from pathlib import Path
 
 MI355X_HBM_BYTES = 288 * 10 ** 9
@@ -114,7 +120,189 @@ def verify_layers(layer_types, actual_ids) -> None:
         raise RuntimeError(f"Incomplete OSCAR layers: expected={sorted(expected)}, actual={sorted(actual_ids)}")
 
 
+# vLLM v1 worker classes on ROCm (the reference hooks vllm_ascend's
+# NPUWorker / NPUModelRunner at the same two methods).
+WORKER_CLASS = ("vllm.v1.worker.gpu_worker", "Worker")
+RUNNER_CLASS = ("vllm.v1.worker.gpu_model_runner", "GPUModelRunner")
+KV_CACHE_UTILS = "vllm.v1.core.kv_cache_utils"
+READY_MARKER = "[oscar-amd] READY "
+INJECTION_FAILED = "[oscar-amd] injection failed"
+
+
+def _import_attr(module: str, name: str):
+    mod = __import__(module, fromlist=[name])
+    return getattr(mod, name)
+
+
+def _oscar_modules(ctx: dict) -> dict:
+    return {name: m for name, m in ctx.items() if getattr(getattr(m, "impl", None), "_oscar_cfg", None) is not None}
+
+
+def oscar_fixed_bytes(runner, specs: dict, targets: dict) -> int:
+    """Persistent bytes the OSCAR layers allocate after profiling (rotations,
+    MFMA operands, window arena and its images, at the engine page size),
+    plus the split-decode workspace of the largest batch, once per device."""
+    fixed = 0
+    hk = heads = 1
+    for name, module in targets.items():
+        impl = module.impl
+        c = impl._oscar
+        bs = specs[name].block_size
+        fixed += fixed_bytes_per_layer(impl.head_size, impl.num_kv_heads, bs, c.sink_tokens, c.recent_tokens,
+                                       c.staging_tokens, c.window_enabled)
+        hk, heads = impl.num_kv_heads, impl.num_heads
+    cfg = runner.vllm_config
+    max_reqs = int(getattr(cfg.scheduler_config, "max_num_seqs", 256) or 256)
+    max_len = int(getattr(cfg.model_config, "max_model_len", 0) or 0)
+    spec_cfg = getattr(cfg, "speculative_config", None)
+    max_q = 1 + int(getattr(spec_cfg, "num_speculative_tokens", 0) or 0) if spec_cfg is not None else 1
+    if targets and max_len > 0:
+        fixed += decode_workspace_bytes(max_reqs, hk, heads, max_q, max_len)
+    return fixed
+
+
 def install_runner_hooks() -> None:
-    """Engine worker seams (reference integration.py:47-195) are engine-build
-    specific; the vLLM-ROCm worker hooks are not wired in this build."""
-    return None
+    """integration.py:47-195 — the two engine seams around cache allocation.
+
+    * ``Worker.determine_available_memory``: the KV budget the engine may
+      allocate shrinks to whole native blocks that fit after the OSCAR
+      persistent buffers (``memory_budget``); the plan is kept on the runner.
+    * ``GPUModelRunner.initialize_kv_cache_tensors``: after the engine built
+      its caches, every OSCAR layer binds them, loads its rotations (and MFMA
+      operands) and allocates its window arena; the actual persistent bytes
+      must stay inside the profiled budget, every full-attention layer must
+      run OSCAR (``verify_layers``), and one READY manifest line is printed.
+
+    The reference's MTP draft shadow caches (``mtp_shadow``) are not part of
+    this build, so the shadow term is zero.  Idempotent."""
+    try:
+        Worker = _import_attr(*WORKER_CLASS)
+        Runner = _import_attr(*RUNNER_CLASS)
+    except Exception as e:  # noqa: BLE001 - no vLLM in this process
+        raise RuntimeError(f"OSCAR runner hooks need vLLM's v1 worker ({e})") from e
+    if getattr(Worker, "_oscar_memory_hook", False):
+        return
+    original_memory = Worker.determine_available_memory
+    original_caches = Runner.initialize_kv_cache_tensors
+
+    def determine_available_memory(worker):
+        available = original_memory(worker)
+        runner = worker.model_runner
+        ctx = runner.compilation_config.static_forward_context
+        targets = _oscar_modules(ctx)
+        if not targets:
+            return available
+        get_groups = _import_attr(KV_CACHE_UTILS, "get_kv_cache_groups")
+        get_config = _import_attr(KV_CACHE_UTILS, "get_kv_cache_config_from_groups")
+        cfg = runner.vllm_config
+        if getattr(cfg.cache_config, "num_gpu_blocks_override", None) is not None:
+            raise ValueError("num_gpu_blocks_override bypasses OSCAR memory budgeting")
+        if getattr(cfg.parallel_config, "data_parallel_size", 1) != 1:
+            raise ValueError("OSCAR manifest validation supports DP=1")
+        if getattr(cfg.parallel_config, "pipeline_parallel_size", 1) != 1:
+            raise ValueError("OSCAR memory accounting supports PP=1")
+        specs = deepcopy(runner.get_kv_cache_spec())
+        groups = get_groups(cfg, deepcopy(specs))
+        provisional = get_config(cfg, groups, available)
+        if provisional.num_blocks < 1:
+            raise ValueError("No native cache blocks fit")
+        native = sum(t.size for t in provisional.kv_cache_tensors) // provisional.num_blocks
+        fixed = oscar_fixed_bytes(runner, specs, targets)
+        budget = memory_budget(available, native, 0, fixed)
+        runner._oscar_memory_plan = {"available": available, "native": native, "shadow": 0, "fixed": fixed,
+                                     "budget": budget}
+        worker.available_kv_cache_memory_bytes = budget
+        print("[oscar-amd] MEMORY " + json.dumps(runner._oscar_memory_plan, sort_keys=True), flush=True)
+        return budget
+
+    def initialize_kv_cache_tensors(runner, kv_cache_config, *args, **kwargs):
+        caches = original_caches(runner, kv_cache_config, *args, **kwargs)
+        from .rotation import layer_index_from_name
+
+        ctx = runner.compilation_config.static_forward_context
+        names, ids = [], []
+        persistent = 0
+        for name, module in _oscar_modules(ctx).items():
+            impl = module.impl
+            cache = caches[name]
+            impl._set_caches(cache)
+            k_cache = impl.key_cache
+            impl._layer_rots(module, k_cache.device)
+            persistent += 4 * impl.head_size ** 2 * 4 + 2 * ROTATION_OPERAND_BYTES
+            if impl._oscar.window_enabled:
+                impl._ensure_staging(module, (impl.key_cache, impl.value_cache))
+                for attr in ("_oscar_stage_k", "_oscar_stage_v", "_oscar_slot_owner", "_oscar_seat_winner",
+                             "_oscar_stage_kimg", "_oscar_stage_vimg"):
+                    t = getattr(module, attr, None)
+                    if t is not None:
+                        persistent += t.numel() * t.element_size()
+            names.append(name)
+            ids.append(layer_index_from_name(name))
+        if names:
+            plan = getattr(runner, "_oscar_memory_plan", None)
+            if plan is None:
+                raise RuntimeError("OSCAR caches were initialised without the OSCAR memory plan")
+            native_bytes = sum(t.size for t in kv_cache_config.kv_cache_tensors)
+            if native_bytes + persistent > plan["available"]:
+                raise RuntimeError("Actual OSCAR persistent allocation exceeds profiled budget")
+            hf = runner.model_config.hf_text_config
+            verify_layers(getattr(hf, "layer_types", []), ids)
+            rank = 0
+            try:
+                import torch.distributed as dist
+
+                rank = dist.get_rank() if dist.is_initialized() else 0
+            except Exception:  # noqa: BLE001 - no process group
+                rank = 0
+            manifest = {
+                "rank": rank,
+                "world_size": runner.vllm_config.parallel_config.tensor_parallel_size,
+                "layers": sorted(names),
+                "layer_ids": sorted(ids),
+                "shadow_layers": [],
+                "native_bytes": native_bytes,
+                "persistent_bytes": persistent,
+                "source": str(Path(__file__).parent.resolve()),
+                "sha256": source_fingerprint(),
+                "verified": True,
+            }
+            runner._oscar_manifest = manifest
+            print(READY_MARKER + json.dumps(manifest, sort_keys=True), flush=True)
+        return caches
+
+    Worker.determine_available_memory = determine_available_memory
+    Runner.initialize_kv_cache_tensors = initialize_kv_cache_tensors
+    Worker._oscar_memory_hook = True
+
+
+
+def validate_ready(log: str, expected_sha: str | None = None) -> dict:
+    """delivery/check_ready.py:8-29 — the READY manifests of a server log, by rank.
+
+    Every tensor-parallel rank must have printed one verified, non-empty
+    manifest; the ranks must agree on world size and layer coverage; each
+    manifest's source fingerprint must equal ``expected_sha`` (or the first
+    rank's); and the log must hold no injection failure or traceback."""
+    records = {}
+    for line in log.splitlines():
+        at = line.find(READY_MARKER)
+        if at < 0:
+            continue
+        record = json.loads(line[at + len(READY_MARKER):])
+        if not record.get("verified") or not record.get("layers"):
+            raise ValueError("Unverified or empty layer manifest")
+        records[record["rank"]] = record
+    if not records:
+        raise ValueError("No verified cache initialization manifests")
+    first = next(iter(records.values()))
+    if set(records) != set(range(first["world_size"])):
+        raise ValueError("Missing tensor-parallel rank manifests")
+    want_sha = expected_sha or first["sha256"]
+    for record in records.values():
+        if record["world_size"] != first["world_size"] or record["layers"] != first["layers"]:
+            raise ValueError("Ranks disagree about model coverage")
+        if record["sha256"] != want_sha:
+            raise ValueError("Worker source does not match this checkout")
+    if INJECTION_FAILED in log or "Traceback (most recent call last)" in log:
+        raise ValueError("Server log contains initialization/runtime failure")
+    return records

@@ -10,7 +10,9 @@ the same seam as the reference (oscar_ascend/plugin.py:73-181, pyproject.toml:12
 3. ``install_impl`` swaps the impl's class to a subclass of
    (OscarAttentionBackendImpl, native impl class) and runs ``_oscar_setup``;
    on any error the original class and ``__dict__`` are restored and the
-   construction fails loudly.
+   construction fails loudly;
+4. the worker hooks (``integration.install_runner_hooks``) are installed
+   once; failing to install them fails the construction the same way.
 
 The reference's Ascend platform bootstrap (plugin.py:27-57) has no MI355X
 counterpart: vLLM resolves the ROCm platform itself.
@@ -86,15 +88,12 @@ def load_plugin() -> None:
             return None
         try:
             install_impl(impl, oscar_class_for(type(impl)))
-        except Exception as e:
-            _HEARTBEAT["errors"].append(str(e))
-            raise RuntimeError(f"[oscar-amd] injection failed: {getattr(self, 'layer_name', '?')}: {e}") from e
-        try:
             from .integration import install_runner_hooks
 
             install_runner_hooks()
-        except Exception as e:  # noqa: BLE001 - budgeting hooks are optional per engine build
-            _HEARTBEAT["errors"].append(f"runner hooks: {e}")
+        except Exception as e:
+            _HEARTBEAT["errors"].append(str(e))
+            raise RuntimeError(f"[oscar-amd] injection failed: {getattr(self, 'layer_name', '?')}: {e}") from e
         _HEARTBEAT["loaded"] += 1
         _HEARTBEAT["layers"].append(
             f"{getattr(self, 'layer_name', '?')}:heads={impl.num_heads}/kv={impl.num_kv_heads}/d={impl.head_size}")
