@@ -14,6 +14,10 @@ the same seam as the reference (oscar_ascend/plugin.py:73-181, pyproject.toml:12
 4. the worker hooks (``integration.install_runner_hooks``) are installed
    once; failing to install them fails the construction the same way.
 
+With ``OSCAR_ASCEND_CALIB=1`` (rotation calibration, ``oscar_amd.gen_rotations``)
+no impl is swapped: every decoder full-attention module gets the capture
+hook of ``oscar_amd.calib`` instead, whatever ``OSCAR_ASCEND_ENABLE`` says.
+
 The reference's Ascend platform bootstrap (plugin.py:27-57) has no MI355X
 counterpart: vLLM resolves the ROCm platform itself.
 """
@@ -69,7 +73,7 @@ def load_plugin() -> None:
     global _PATCHED
     if _PATCHED:
         return
-    if os.environ.get("OSCAR_ASCEND_ENABLE", "auto") == "0":
+    if os.environ.get("OSCAR_ASCEND_ENABLE", "auto") == "0" and not _calibrating():
         print("[oscar-amd] OSCAR_ASCEND_ENABLE=0 -> native attention kept")
         _PATCHED = True
         return
@@ -83,6 +87,16 @@ def load_plugin() -> None:
 
     def _patched_init(self, *args, **kwargs):
         orig_init(self, *args, **kwargs)
+        if _calibrating():
+            # plugin.py:103-111: calibration keeps the native impl and only
+            # captures the unquantized Q/K/V of the engine's forward passes
+            try:
+                from .calib import register_attention_hook
+
+                register_attention_hook(self)
+            except Exception as e:  # noqa: BLE001 - a layer without captures is reported by finalize_cov
+                print(f"[oscar-amd] calibration hook not registered on {getattr(self, 'layer_name', '?')}: {e}")
+            return None
         impl = getattr(self, "impl", None)
         if impl is None or not _should_oscar(self, impl):
             return None
@@ -102,6 +116,10 @@ def load_plugin() -> None:
     Attention.__init__ = _patched_init
     _PATCHED = True
     print("[oscar-amd] plugin loaded: Attention.__init__ after-hook installed")
+
+
+def _calibrating() -> bool:
+    return os.environ.get("OSCAR_ASCEND_CALIB", "0") == "1"
 
 
 def _is_hybrid_config(model_config) -> bool:
