@@ -162,16 +162,58 @@ def decode_bytes(st: LayerState) -> dict:
             "int2_160B_variant": hist_tokens * HK * 160 + fixed}
 
 
-def bench_decode(args, dev, history, q_len, pool, layers, seed=93):
+def decode_only_bytes(st: LayerState) -> dict:
+    """Algorithmic HBM bytes of one DecodeOnly read: every history position's
+    INT2 slot bytes, the staged fp32 K/V of the positions the windowed read
+    takes from the arena (the sink when all of its seats hold it, the staged
+    run ending at the last position inside the recent window), the owner
+    entries of the sink and tail pages, q and out in fp32, block-table entries."""
+    import torch
+
+    stage = st.stage()
+    bt = st.bt.cpu()
+    cfg = st.impl._oscar
+    n_q = st.q_rot.shape[0]
+    used = hist_tokens = owner_entries = 0
+    for i, seq in enumerate(st.seqs):
+        hist_tokens += seq
+        if stage is None:
+            continue
+        owner = stage[2].cpu()
+        pos = torch.arange(seq)
+        pages = bt[i][pos // BS].long()
+        staged = owner[pages % owner.shape[0], pos % BS] == pages
+        sink = (cfg.sink_tokens // BS) * BS
+        head = sink if 0 < sink < seq and bool(staged[:sink].all()) else 0
+        t0 = max(seq - cfg.recent_tokens, head)
+        cut = seq
+        while cut > t0 and bool(staged[cut - 1]):
+            cut -= 1
+        used += head + (seq - cut)
+        owner_entries += head + (seq - t0)
+    int2 = hist_tokens * HK * 136
+    fixed = used * HK * 2 * D * 4 + owner_entries * 8 + 2 * n_q * HQ * D * 4 + \
+        sum((s + BS - 1) // BS for s in st.seqs) * 4
+    return {"total": int2 + fixed, "int2": int2, "window": used * HK * 2 * D * 4, "staged_tokens": used,
+            "int2_160B_variant": hist_tokens * HK * 160 + fixed}
+
+
+def bench_decode(args, dev, history, q_len, pool, layers, seed=93, decode_only=False):
     import torch
 
     from oscar_amd.kernels import decode
 
     base = build_layer(dev, history, q_len, pool, seed, window=bool(args.window))
-    nbytes = decode_bytes(base)
+    nbytes = decode_only_bytes(base) if decode_only else decode_bytes(base)
     states = [base] + [clone_layer(base) for _ in range(layers - 1)]
-    plans = [decode.plan(st.q_rot, st.k_rot, st.v_rot, st.caches[0], st.caches[1], st.bt, st.qsl,
-                         st.seqs, st.impl.scale, st.stage(), tiles_per_split=args.tps) for st in states]
+    if decode_only:
+        cfg = base.impl._oscar
+        plans = [decode.decode_only_plan(st.q_rot, st.caches[0], st.caches[1], st.bt, st.seqs, st.impl.scale,
+                                         st.stage(), cfg.sink_tokens, cfg.recent_tokens, tiles_per_split=args.tps)
+                 for st in states]
+    else:
+        plans = [decode.plan(st.q_rot, st.k_rot, st.v_rot, st.caches[0], st.caches[1], st.bt, st.qsl,
+                             st.seqs, st.impl.scale, st.stage(), tiles_per_split=args.tps) for st in states]
     torch.cuda.synchronize()
     side = torch.cuda.Stream(dev)
     side.wait_stream(torch.cuda.current_stream(dev))
@@ -283,6 +325,39 @@ def traffic_from_profile(kernel_src: Path):
         return None
 
 
+def decode_only_cpu_baseline(st, gpu_out, seconds: float):
+    """The oracle's DecodeOnly read (INT2 middle + FP32 sink/tail, LSE merge) on
+    the same GPU-written state, on this host, and the parity of the timed kernel
+    against it (fp32 contract for this read: 2e-3 relative to the output scale)."""
+    import torch
+
+    from oracle import attention as oatt
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    q, kc, vc, bt = st.q_rot.cpu(), st.caches[0].cpu(), st.caches[1].cpu(), st.bt.cpu()
+    stage = st.stage()
+    cfg = st.impl._oscar
+    arena = None
+    if stage is not None:
+        arena = (stage[0].cpu(), stage[1].cpu(), stage[2].cpu(), (cfg.sink_tokens // BS) * BS, cfg.recent_tokens)
+
+    def once():
+        return oatt.decode_only_ref(q, kc, vc, bt, st.seqs, st.impl.scale, HK, D, arena)
+
+    want = once()
+    rel = (gpu_out.cpu() - want).abs().max().item() / max(want.abs().max().item(), 1e-30)
+    samples = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(samples) < 6:
+        t0 = time.perf_counter()
+        once()
+        samples.append(time.perf_counter() - t0)
+    return {"value": round(statistics.median(samples) * 1e6, 1), "unit": "us/layer", "cores": cores,
+            "kind": "port", "sample": f"median of {len(samples)} runs of the oracle DecodeOnly read on the same "
+                                      f"state ({sum(st.seqs)}-token INT2 history, FP32 sink + tail, fp32)"}, rel
+
+
 def cpu_baseline(st, gpu_out, seconds: float, label: str = "C2"):
     """The oracle's read path on the same (GPU-written) C2 state, on this host.
 
@@ -332,6 +407,10 @@ SUITE = {
                               "pages scattered over a 2056-page pool (2048 history pages + 8 for the step's "
                               "token), FP32 sink=128/recent=256 window (staging 8192), 16 distinct layers",
                   "q_len": 1, "pool": 2056, "layers": 16},
+    "C2-decode-only": {"workload": "C2 DecodeOnly: the read without fresh K/V, 1 request x 1 query token over "
+                                   "its whole 24580-token INT2 history in 193 shuffled 128-token pages, Hq=6 "
+                                   "Hk=1 D=256, FP32 sink=128/recent=256 window (staging 8192), 64 distinct layers",
+                       "q_len": 1, "pool": 193, "layers": 64, "decode_only": True},
     "C4": {"workload": "C4: prefill continuation, 1 request, 15360-token INT2 history + 9256 new tokens "
                        "(causal over history + new), Hq=6 Hk=1 D=256, 128-token pages, FP32 window"},
 }
@@ -344,6 +423,8 @@ def suite_histories(name: str):
     if name == "C3":
         g = torch.Generator().manual_seed(2024)
         return [int(x) for x in torch.randint(2048, 16385, (32,), generator=g)]
+    if name == "C2-decode-only":
+        return [24579]
     return [32768] * 8
 
 
@@ -422,16 +503,22 @@ def suite(args, dev):
                     "parity_max_abs_err": err, "cpu_baseline": cpu}
         else:
             hist = suite_histories(name)
-            dec = bench_decode(args, dev, hist, cfg["q_len"], pool=cfg["pool"], layers=cfg["layers"])
-            cpu, rel = cpu_baseline(dec["state"], dec["out0"], args.cpu_seconds, name)
-            if not rel <= 1e-3:
+            only = cfg.get("decode_only", False)
+            dec = bench_decode(args, dev, hist, cfg["q_len"], pool=cfg["pool"], layers=cfg["layers"],
+                               decode_only=only)
+            if only:
+                cpu, rel = decode_only_cpu_baseline(dec["state"], dec["out0"], args.cpu_seconds)
+            else:
+                cpu, rel = cpu_baseline(dec["state"], dec["out0"], args.cpu_seconds, name)
+            if not rel <= (2e-3 if only else 1e-3):
                 raise SystemExit(f"{name} parity gate failed: rel err {rel:.3e}")
             line = {"config": name, "workload": cfg["workload"], "value": round(dec["us_per_layer"], 3),
                     "unit": "us/layer", "steps": dec["steps"],
                     "roofline": {"bound": "hbm", "achieved": round(dec["gbps"], 1), "peak": HBM_PEAK_GBPS,
                                  "unit": "GB/s", "frac": round(dec["gbps"] / HBM_PEAK_GBPS, 4),
                                  "bytes_per_layer": dec["bytes"]["total"]},
-                    "history_tokens": sum(hist), "staged_tokens": dec["bytes"]["staged_tokens"],
+                    "history_tokens": sum(dec["state"].seqs) if only else sum(hist),
+                    "staged_tokens": dec["bytes"]["staged_tokens"],
                     "parity_rel_err": rel, "cpu_baseline": cpu}
         print(json.dumps(line), flush=True)
 
@@ -451,8 +538,8 @@ def main():
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run a plain device copy of this many MiB first (PMC byte-counter calibration)")
     ap.add_argument("--suite", default="",
-                    help="comma list of extra workloads (C3, C5-decode, C4): one JSON line each instead "
-                         "of the headline line")
+                    help="comma list of extra workloads (C3, C5-decode, C2-decode-only, C4): one JSON "
+                         "line each instead of the headline line")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (one TP rank's share "

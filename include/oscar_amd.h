@@ -123,6 +123,38 @@ int oscar_paged_decode(const float* q_rot, const float* k_new, const float* v_ne
                        int32_t tiles_per_split, float* out, void* workspace,
                        size_t workspace_size, oscar_stream_t stream);
 
+/* ---------------------------------------------------------------- DecodeOnly decode
+ * One query token per request over its whole history [0, seq_lens[i]) when
+ * the step brings no fresh K/V (key = None).  Replaces
+ * AscendOscarAttentionBackendImpl._decode_attention and
+ * _decode_attention_windowed (oscar_ascend/backend.py:321-358, 500-611:
+ * oscar_decode_triton over the INT2 middle, FP32 sink + staged tail, LSE
+ * merge; kernels/decode_kernel.py:41-67, 250-293).
+ *   q_rot [num_requests][Hq][D] fp32 rotated; out [num_requests][Hq][D] fp32
+ *   rotated-V; seq_lens [num_requests] int32 in HOST memory; caches, block
+ *   table and staging as in oscar_paged_decode.  With an arena
+ *   (stage_rows > 0) the staged value of position p is used only where the
+ *   reference's windowed decode uses it: p < sink_eff when the request is
+ *   longer than sink_eff = (sink_tokens / block_size) * block_size and every
+ *   seat of its sink pages holds its page, and p >= cut, where [cut, seq)
+ *   is the run of staged positions ending at seq - 1 inside
+ *   [max(seq - recent_tokens, sink end), seq).  Elsewhere the INT2 value.
+ *   workspace: >= oscar_decode_only_workspace_bytes(...) bytes (same
+ *   tiles_per_split).
+ */
+size_t oscar_decode_only_workspace_bytes(int32_t num_requests, int32_t num_kv_heads, int32_t num_heads,
+                                         int64_t max_history, int32_t tiles_per_split);
+int oscar_decode_only(const float* q_rot, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+                      const void* k_cache, const void* v_cache, int32_t block_size, int64_t num_pages,
+                      int64_t k_stride_page, int64_t k_stride_token, int64_t k_stride_head,
+                      int64_t v_stride_page, int64_t v_stride_token, int64_t v_stride_head,
+                      const int32_t* block_table, int64_t block_table_stride, int32_t block_table_cols,
+                      const int32_t* seq_lens, int32_t num_requests, int64_t max_history,
+                      const int64_t* stage_owner, const void* stage_k_image, const void* stage_v_image,
+                      int32_t stage_rows, int32_t sink_tokens, int32_t recent_tokens, float scale,
+                      int32_t tiles_per_split, float* out, void* workspace, size_t workspace_size,
+                      oscar_stream_t stream);
+
 /* ---------------------------------------------------------------- prefill continuation
  * Causal attention of one request's num_new new tokens over its cached_len
  * INT2 history tokens plus themselves (new token j sees keys 0 .. cached_len

@@ -133,3 +133,81 @@ def merge_splits(outs: torch.Tensor, lses: torch.Tensor):
     if total <= 0.0:
         return torch.zeros_like(acc), -math.inf
     return acc / total, m + math.log(total)
+
+
+def window_bounds(owner, bt_row, seq: int, bs: int, sink_eff: int, recent: int):
+    """backend.py:514-551 — (sink_active, cut) of one DecodeOnly request.
+
+    The sink counts only when the request is longer than it and every seat of
+    its sink pages holds that page; the tail is the longest run of staged
+    positions ending at seq - 1 inside [max(seq - recent, sink end), seq);
+    cut is where that run starts (seq when position seq - 1 is not staged).
+    """
+    rows = owner.shape[0]
+
+    def staged(pos):
+        page = int(bt_row[pos // bs])
+        return int(owner[page % rows, pos % bs]) == page
+
+    sink_pages = sink_eff // bs
+    sink_active = sink_pages > 0 and seq > sink_eff and all(staged(p) for p in range(sink_pages * bs))
+    t0 = max(seq - recent, sink_eff if sink_active else 0)
+    cut = seq
+    while cut > t0 and staged(cut - 1):
+        cut -= 1
+    return sink_active, cut
+
+
+def _segment(q, k, v, scale: float, g: int):
+    """Softmax attention of q [Hq, D] over k, v [L, Hk, D]: (out [Hq, D], lse [Hq]);
+    an empty segment gives (0, -inf)."""
+    if k.shape[0] == 0:
+        return torch.zeros_like(q), torch.full((q.shape[0],), -math.inf)
+    s = torch.einsum("hd,lhd->hl", q, k.repeat_interleave(g, dim=1)) * scale
+    return torch.einsum("hl,lhd->hd", torch.softmax(s, -1), v.repeat_interleave(g, dim=1)), torch.logsumexp(s, -1)
+
+
+def decode_only_ref(q, kc, vc, bt, seqs, scale: float, hk: int, D: int, arena=None):
+    """backend.py:321-358, 500-586 — the DecodeOnly read (no fresh K/V): one
+    rotated query per request [B, Hq, D] over its whole history [0, seq).
+
+    Without a window arena: decode_ref over the INT2 caches.  With one
+    (``arena``: stage_k, stage_v, owner, sink_eff, recent): the INT2 middle
+    [si*bs, cut), read through the block table shifted by si sink pages, and
+    the FP32 segment (sink positions when the sink is active, tail [cut, seq))
+    are attended separately and merged through their log-sum-exps.
+    Output fp32 in the rotated-V domain.
+    """
+    B, Hq, _ = q.shape
+    g = Hq // hk
+    if arena is None:
+        return decode_ref(q, kc, vc, bt, torch.tensor(seqs), scale, hk, D)[0]
+    sk, sv, owner, sink_eff, recent = arena
+    bs = kc.shape[1]
+    rows = owner.shape[0]
+    out = torch.zeros(B, Hq, D)
+    for b, seq in enumerate(seqs):
+        row = bt[b].long()
+        sink_active, cut = window_bounds(owner, row, seq, bs, sink_eff, recent)
+        si = sink_eff // bs if sink_active else 0
+        # INT2 middle
+        n_mid = cut - si * bs
+        if n_mid > 0:
+            shifted = row[torch.clamp(torch.arange(row.numel()) + si, max=row.numel() - 1)]
+            o1, l1 = decode_ref(q[b:b + 1].float(), kc, vc, shifted[None], [n_mid], scale, hk, D)
+            o1, l1 = torch.nan_to_num(o1[0]), l1[0]
+            l1 = torch.where(torch.isfinite(l1), l1, torch.full_like(l1, -math.inf))
+        else:
+            o1, l1 = torch.zeros(Hq, D), torch.full((Hq,), -math.inf)
+        # FP32 sink + tail from the arena
+        pos = list(range(sink_eff)) if sink_active else []
+        pos += list(range(cut, seq))
+        p = torch.tensor(pos, dtype=torch.long)
+        pages = row[p // bs] if pos else p
+        ks = sk[pages % rows, p % bs] if pos else torch.zeros(0, hk, D)
+        vs = sv[pages % rows, p % bs] if pos else torch.zeros(0, hk, D)
+        o2, l2 = _segment(q[b].float(), ks.float(), vs.float(), scale, g)
+        lse = torch.logaddexp(l1, l2)
+        safe = torch.where(torch.isfinite(lse), lse, torch.zeros_like(lse))
+        out[b] = o1 * torch.exp(l1 - safe)[:, None] + torch.nan_to_num(o2) * torch.exp(l2 - safe)[:, None]
+    return out

@@ -73,6 +73,13 @@ class OscarAttentionState(Enum):
     SpecDecoding = 4
 
 
+def _is_decode_only(state) -> bool:
+    """The DecodeOnly member of any engine's attention-state enum (or its value 2)."""
+    if state is None:
+        return False
+    return getattr(state, "name", None) == "DecodeOnly" or state == OscarAttentionState.DecodeOnly.value
+
+
 class OscarAttentionBackendImpl:
     """Mixed into the native FULL-attention impl class by the plugin."""
 
@@ -234,7 +241,14 @@ class OscarAttentionBackendImpl:
             return output.fill_(0)
         self._set_caches(kv_cache)
         if key is None or value is None:
-            raise NotImplementedError("OSCAR reads need the step's fresh K/V (MTP / prefill routes)")
+            # backend.py:304-309: without fresh K/V only the DecodeOnly state
+            # has a read path (the reference's dense route needs the keys)
+            if not _is_decode_only(getattr(attn_metadata, "attn_state", None)):
+                raise NotImplementedError("OSCAR reads without fresh K/V need the DecodeOnly attention state")
+            attn_out = self._decode_attention(layer, query, attn_metadata)
+            self._oscar_stats["reads"] += 1
+            output[:num_tokens] = attn_out.reshape(output[:num_tokens].shape).to(output.dtype)
+            return output
 
         self.do_kv_cache_update(layer, key, value, kv_cache,
                                 attn_metadata.slot_mapping[:attn_metadata.num_actual_tokens])
@@ -249,6 +263,23 @@ class OscarAttentionBackendImpl:
         else:
             output[:num_tokens] = attn_out.reshape(num_tokens, -1).to(output.dtype)
         return output
+
+    def _decode_attention(self, layer, query, attn_metadata) -> torch.Tensor:
+        """backend.py:321-358, 500-586 — one query token per request over its
+        whole history, staged values only in the windowed segments; output
+        in the query dtype."""
+        qsl, seqs = metadata_batch_lists(attn_metadata)
+        N = query.shape[0]
+        B = len(seqs)
+        if N != B or any(b - a != 1 for a, b in itertools.pairwise(qsl[:B + 1])):
+            raise ValueError("DecodeOnly needs exactly one query token per request")
+        dev = query.device
+        rk, _ = self._layer_rots(layer, dev)
+        cfg = self._oscar
+        q = query.reshape(N, self.num_heads, self.head_size)
+        out_rot = decode.decode_only(q.float() @ rk, self.key_cache, self.value_cache, attn_metadata.block_tables,
+                                     seqs, self.scale, self._stage(layer), cfg.sink_tokens, cfg.recent_tokens)
+        return (out_rot @ layer._oscar_rvT).to(query.dtype)
 
     def _read(self, layer, query, key, value, attn_metadata) -> torch.Tensor:
         N, Hq, D = query.shape

@@ -50,6 +50,14 @@
 //    head) against new tokens 0 .. j), written as one more partial.
 // merge kernel: one 256-thread block per (output row, feature quarter) of an
 //   item; LSE-combines the item's partials and writes that slice of the row.
+//
+// DecodeOnly read (no fresh K/V; one query token per request, history
+// [0, seq)): the same kernels without the fresh-token workgroup, and a
+// staged value replaces the INT2 one only at positions p < head or p >= cut
+// of the request.  A bounds kernel computes (head, cut) on the device first:
+// head is the sink length when every seat of the sink pages holds its page,
+// else 0; cut starts the run of staged positions that ends at seq - 1 inside
+// [max(seq - recent, head), seq).
 #include "oscar_common.h"
 
 namespace oscar {
@@ -106,6 +114,8 @@ struct DecodeArgs {
   float scale_log2;             // attention scale * log2(e)
   float* out;                   // [n, Hq, D]
   float* ws;                    // partials
+  const int32_t* win;           // DecodeOnly: (head, cut) per chunk request; null: every position
+  int32_t fresh;                // 1: the fresh-token partial exists (MTP read); 0: DecodeOnly
   int32_t max_splits, row_tiles;
   ItemInfo items[kMaxInlineItems];
 };
@@ -379,7 +389,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   const int rows = it.nq * a.group;
   if (it.nq <= 0 || rt * kRows >= rows) return;
   if (split == a.max_splits) {
-    fresh_partial(a, it, item, rt, *reinterpret_cast<FreshLds*>(smem_raw));
+    if (a.fresh) fresh_partial(a, it, item, rt, *reinterpret_cast<FreshLds*>(smem_raw));
     return;
   }
   const int prefix = it.prefix;
@@ -396,6 +406,16 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   const int nsplit = a.max_splits;
   const int nst = (steps - 1 - split) / nsplit + 1;     // steps split + nsplit k, k < nst (<= 64)
   const bool arena = a.stage_rows > 0;
+  // Positions whose staged value may replace the INT2 one: p < win_head or
+  // p >= win_tail (every position for the MTP read).  Scalar loads, waited
+  // for with the LDS barrier below.
+  int win_head = 0, win_tail = 0;
+  if (a.win) {
+    typedef __attribute__((address_space(4))) const int32_t const_i32;
+    const const_i32* wb = (const const_i32*)a.win;
+    win_head = wb[2 * it.req];
+    win_tail = wb[2 * it.req + 1];
+  }
 
   // ---- requests before any wait: the query features, then the pages of the
   // workgroup's tiles (lane k of pgv[j]: tile j of step k), then the first
@@ -495,8 +515,9 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
     if (arena) {
       const int pa = g == 0 ? pgs[0] : pgs[1];
       const int pb = g == 0 ? pgs[2] : pgs[3];
-      const bool s0 = pa >= 0 && tbase + lane < prefix && L.own0 == pa;
-      const bool s1 = pb >= 0 && tbase + 64 + lane < prefix && L.own1 == pb;
+      const int q0 = tbase + lane, q1 = tbase + 64 + lane;
+      const bool s0 = pa >= 0 && q0 < prefix && (q0 < win_head || q0 >= win_tail) && L.own0 == pa;
+      const bool s1 = pb >= 0 && q1 < prefix && (q1 < win_head || q1 >= win_tail) && L.own1 == pb;
       const uint64_t b0 = __ballot(s0), b1 = __ballot(s1);
       wm0 = (uint32_t)b0;
       wm1 = (uint32_t)(b0 >> 32);
@@ -799,7 +820,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
   const int sg = tid >> 4, fl = tid & 15;
   const int steps = (it.prefix + kStepTok - 1) / kStepTok;
   const int hs = min(a.max_splits, steps);        // history partials 0 .. hs - 1
-  const int P = hs + 1;                           // partial hs is the fresh one (split max_splits)
+  const int P = hs + a.fresh;                     // partial hs is the fresh one (split max_splits)
   const float* base = a.ws + item_index(a, item, 0, rt) * kPartialFloats;
   const int64_t pstride = (int64_t)a.row_tiles * kPartialFloats;
   const int f0 = 64 * qd + 4 * fl;
@@ -891,6 +912,70 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
   }
 }
 
+// DecodeOnly window bounds of the launch chunk's requests (backend.py:514-551):
+// win[2r] = head (sink_eff when the request is longer than the sink and every
+// seat of its sink pages holds that page, else 0), win[2r + 1] = cut (start of
+// the run of staged positions ending at seq - 1 inside [t0, seq), t0 =
+// max(seq - recent, head); seq when position seq - 1 is not staged).  With h
+// the highest position in [max(seq - recent, 0), seq) that is not staged,
+// cut = h + 1 if h >= t0, else t0.  One 256-thread block per request; every
+// position is checked by its own thread (block-table entries outside
+// [0, num_pages) count as not staged).
+constexpr int kBoundsThreads = 256;
+
+__global__ __launch_bounds__(kBoundsThreads) void decode_only_bounds_kernel(DecodeArgs a, int32_t* __restrict__ win,
+                                                                            int32_t sink_eff, int32_t recent) {
+  __shared__ int32_t sink_bad[kBoundsThreads / 64];
+  __shared__ int32_t top_bad[kBoundsThreads / 64];
+  const int r = blockIdx.x;
+  const ItemInfo it = a.items[r * a.num_kv_heads];
+  const int seq = it.prefix;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int32_t* bt_row = a.block_table + (int64_t)it.req * a.bt_stride;
+  auto staged = [&](int pos) -> bool {
+    const uint32_t pi = fast_div((uint32_t)pos, a.bs_div);
+    if ((int)pi >= a.bt_cols) return false;
+    const int page = bt_row[pi];
+    if (page < 0 || page >= a.num_pages) return false;
+    const int64_t seat = (int64_t)fast_mod((uint32_t)page, a.rows_div) * a.block_size +
+                         (pos - (int)pi * a.block_size);
+    return a.owner[seat] == (int64_t)page;
+  };
+  const bool sink_len = sink_eff > 0 && seq > sink_eff;
+  bool bad_sink = false;
+  if (sink_len)
+    for (int p = tid; p < sink_eff; p += kBoundsThreads) bad_sink = bad_sink || !staged(p);
+  const int lo = max(seq - recent, 0);
+  int h = -1;                                   // highest unstaged position of this thread
+  for (int p = seq - 1 - tid; p >= lo; p -= kBoundsThreads)
+    if (!staged(p)) {
+      h = p;
+      break;
+    }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) h = max(h, __shfl_xor(h, o, 64));
+  const bool any_bad = __ballot(bad_sink) != 0ull;
+  if (lane == 0) {
+    sink_bad[w] = any_bad;
+    top_bad[w] = h;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    bool sb = false;
+    int hb = -1;
+#pragma unroll
+    for (int k = 0; k < kBoundsThreads / 64; ++k) {
+      sb = sb || sink_bad[k];
+      hb = max(hb, top_bad[k]);
+    }
+    const int head = (sink_len && !sb) ? sink_eff : 0;
+    const int t0 = max(seq - recent, head);
+    win[2 * r] = head;
+    win[2 * r + 1] = hb >= t0 ? hb + 1 : t0;
+  }
+}
+
 int64_t splits_for(int64_t max_history, int tiles_per_split) {
   const int64_t tiles = max_history > 0 ? (max_history + kTile - 1) / kTile : 0;
   return (tiles + tiles_per_split - 1) / tiles_per_split;
@@ -922,6 +1007,72 @@ size_t workspace_floats(int32_t num_requests, int32_t num_kv_heads, int32_t num_
   return (size_t)reqs * num_kv_heads * (splits_for(max_history, tiles_per_split) + 1) * tiles_r *
          kPartialFloats;
 }
+
+// Cache, block-table and arena checks shared by both entries, then the
+// common kernel arguments.  Returns kOk or the error code.
+int fill_common(DecodeArgs& a, const float* q_rot, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+                const void* k_cache, const void* v_cache, int32_t block_size, int64_t num_pages,
+                int64_t k_stride_page, int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
+                int64_t v_stride_token, int64_t v_stride_head, const int32_t* block_table,
+                int64_t block_table_stride, int32_t block_table_cols, int64_t max_history,
+                const int64_t* stage_owner, const void* stage_k_image, const void* stage_v_image,
+                int32_t stage_rows, float scale, float* out, void* workspace) {
+  if (head_size != kHeadDim) return kErrUnsupportedHeadDim;
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_kv_heads > kMaxInlineItems || num_heads % num_kv_heads != 0 ||
+      max_history < 0 || block_size <= 0 || num_pages <= 0 || block_table_cols < 0 || stage_rows < 0)
+    return kErrInvalidArgument;
+  if (!q_rot || !k_cache || !v_cache || !out) return kErrInvalidArgument;
+  if (max_history > 0 && (!block_table || block_table_cols <= 0)) return kErrInvalidArgument;
+  if (stage_rows > 0 && (!stage_owner || !stage_k_image || !stage_v_image)) return kErrInvalidArgument;
+  if (stage_rows > 0 && ((reinterpret_cast<uintptr_t>(stage_k_image) & 15) ||
+                         (reinterpret_cast<uintptr_t>(stage_v_image) & 15)))
+    return kErrInvalidArgument;
+  if (block_size % kTile != 0 || k_stride_head < kKCodeOff + kCodeBytes || v_stride_head < kCodeBytes ||
+      (k_stride_head & 15) || (k_stride_token & 15) || (k_stride_page & 15) || (v_stride_head & 7) ||
+      (v_stride_token & 7) || (v_stride_page & 7) || (reinterpret_cast<uintptr_t>(k_cache) & 15) ||
+      (reinterpret_cast<uintptr_t>(v_cache) & 7))
+    return kErrUnsupportedGeometry;
+  a.q = q_rot;
+  a.k_cache = static_cast<const uint8_t*>(k_cache);
+  a.v_cache = static_cast<const uint8_t*>(v_cache);
+  a.k_page = k_stride_page;
+  a.k_tok = k_stride_token;
+  a.k_head = k_stride_head;
+  a.v_page = v_stride_page;
+  a.v_tok = v_stride_token;
+  a.v_head = v_stride_head;
+  a.block_size = block_size;
+  a.bs_div = make_fast_div((uint32_t)block_size);
+  a.rows_div = make_fast_div(stage_rows > 0 ? (uint32_t)stage_rows : 1u);
+  a.num_pages = num_pages;
+  a.bt_stride = block_table_stride;
+  a.bt_cols = block_table_cols;
+  a.num_heads = num_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.group = num_heads / num_kv_heads;
+  a.owner = stage_owner;
+  a.kimg = static_cast<const _Float16*>(stage_k_image);
+  a.vimg = static_cast<const _Float16*>(stage_v_image);
+  a.stage_rows = stage_rows;
+  a.scale_log2 = scale * kLog2e;
+  a.out = out;
+  a.ws = static_cast<float*>(workspace);
+  return kOk;
+}
+
+int set_split_lds() {
+  static bool lds_attr_set = false;
+  if (!lds_attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(paged_decode_split_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes) != hipSuccess)
+      return kErrLaunch;
+    lds_attr_set = true;
+  }
+  return kOk;
+}
+
+// Bytes of the DecodeOnly bounds array after the partials (256-byte aligned).
+size_t bounds_offset(size_t partial_bytes) { return (partial_bytes + 255) & ~(size_t)255; }
 
 }  // namespace
 }  // namespace oscar
@@ -962,8 +1113,13 @@ int oscar_paged_decode(const float* q_rot, const float* k_new, const float* v_ne
       block_table_cols < 0 || stage_rows < 0 || tiles_per_split < 0 || tiles_per_split > kMaxTilesPerSplit)
     return kErrInvalidArgument;
   if (num_tokens == 0 || num_requests == 0 || max_query_len == 0) return kOk;
-  if (!q_rot || !k_new || !v_new || !k_cache || !v_cache || !query_start_loc || !seq_lens || !out)
-    return kErrInvalidArgument;
+  DecodeArgs a{};
+  int rc = fill_common(a, q_rot, num_heads, num_kv_heads, head_size, k_cache, v_cache, block_size, num_pages,
+                       k_stride_page, k_stride_token, k_stride_head, v_stride_page, v_stride_token, v_stride_head,
+                       block_table, block_table_stride, block_table_cols, max_history, stage_owner, stage_k_image,
+                       stage_v_image, stage_rows, scale, out, workspace);
+  if (rc != kOk) return rc;
+  if (!k_new || !v_new || !query_start_loc || !seq_lens) return kErrInvalidArgument;
   // Host-side request layout (the reference's query_layout checks).
   if (query_start_loc[0] < 0 || query_start_loc[num_requests] > num_tokens) return kErrInvalidArgument;
   for (int32_t i = 0; i < num_requests; ++i) {
@@ -971,16 +1127,6 @@ int oscar_paged_decode(const float* q_rot, const float* k_new, const float* v_ne
     if (nq < 0 || nq > max_query_len || seq_lens[i] < nq || (int64_t)(seq_lens[i] - nq) > max_history)
       return kErrInvalidArgument;
   }
-  if (max_history > 0 && (!block_table || block_table_cols <= 0)) return kErrInvalidArgument;
-  if (stage_rows > 0 && (!stage_owner || !stage_k_image || !stage_v_image)) return kErrInvalidArgument;
-  if (stage_rows > 0 && ((reinterpret_cast<uintptr_t>(stage_k_image) & 15) ||
-                         (reinterpret_cast<uintptr_t>(stage_v_image) & 15)))
-    return kErrInvalidArgument;
-  if (block_size % kTile != 0 || k_stride_head < kKCodeOff + kCodeBytes || v_stride_head < kCodeBytes ||
-      (k_stride_head & 15) || (k_stride_token & 15) || (k_stride_page & 15) || (v_stride_head & 7) ||
-      (v_stride_token & 7) || (v_stride_page & 7) || (reinterpret_cast<uintptr_t>(k_cache) & 15) ||
-      (reinterpret_cast<uintptr_t>(v_cache) & 7))
-    return kErrUnsupportedGeometry;
   const int tps = tiles_per_split > 0 ? tiles_per_split
                                       : default_tiles_per_split(num_requests, num_kv_heads, max_history);
   const int64_t splits = splits_for(max_history, tps);
@@ -988,45 +1134,13 @@ int oscar_paged_decode(const float* q_rot, const float* k_new, const float* v_ne
   const size_t need = workspace_floats(num_requests, num_kv_heads, num_heads, max_query_len, max_history, tps) *
                       sizeof(float);
   if (workspace == nullptr || workspace_size < need) return kErrWorkspaceTooSmall;
-
-  DecodeArgs a{};
-  a.q = q_rot;
   a.k_new = k_new;
   a.v_new = v_new;
-  a.k_cache = static_cast<const uint8_t*>(k_cache);
-  a.v_cache = static_cast<const uint8_t*>(v_cache);
-  a.k_page = k_stride_page;
-  a.k_tok = k_stride_token;
-  a.k_head = k_stride_head;
-  a.v_page = v_stride_page;
-  a.v_tok = v_stride_token;
-  a.v_head = v_stride_head;
-  a.block_size = block_size;
-  a.bs_div = make_fast_div((uint32_t)block_size);
-  a.rows_div = make_fast_div(stage_rows > 0 ? (uint32_t)stage_rows : 1u);
-  a.num_pages = num_pages;
-  a.bt_stride = block_table_stride;
-  a.bt_cols = block_table_cols;
-  a.num_heads = num_heads;
-  a.num_kv_heads = num_kv_heads;
-  a.group = num_heads / num_kv_heads;
-  a.owner = stage_owner;
-  a.kimg = static_cast<const _Float16*>(stage_k_image);
-  a.vimg = static_cast<const _Float16*>(stage_v_image);
-  a.stage_rows = stage_rows;
-  a.scale_log2 = scale * kLog2e;
-  a.out = out;
-  a.ws = static_cast<float*>(workspace);
+  a.win = nullptr;
+  a.fresh = 1;
   a.max_splits = (int32_t)splits;
   a.row_tiles = (max_query_len * a.group + kRows - 1) / kRows;
-
-  static bool lds_attr_set = false;
-  if (!lds_attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(paged_decode_split_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes) != hipSuccess)
-      return kErrLaunch;
-    lds_attr_set = true;
-  }
+  if ((rc = set_split_lds()) != kOk) return rc;
   // Chunks of whole requests (at most kMaxInlineItems items); each chunk's
   // partials reuse the same workspace (the merge of one chunk precedes the
   // next split in stream order).
@@ -1044,6 +1158,86 @@ int oscar_paged_decode(const float* q_rot, const float* k_new, const float* v_ne
     dim3 grid((unsigned)(a.max_splits + 1), nitems, (unsigned)a.row_tiles);
     hipLaunchKernelGGL(paged_decode_split_kernel, grid, dim3(256), kLdsBytes, stream, a);
     if (hipGetLastError() != hipSuccess) return kErrLaunch;
+    dim3 mgrid((unsigned)(kRows * 4), nitems, (unsigned)a.row_tiles);
+    hipLaunchKernelGGL(paged_decode_merge_kernel, mgrid, dim3(256), 0, stream, a);
+    if (hipGetLastError() != hipSuccess) return kErrLaunch;
+  }
+  return kOk;
+}
+
+size_t oscar_decode_only_workspace_bytes(int32_t num_requests, int32_t num_kv_heads, int32_t num_heads,
+                                         int64_t max_history, int32_t tiles_per_split) {
+  const size_t partials = oscar_paged_decode_workspace_bytes(num_requests, num_kv_heads, num_heads, 1,
+                                                             max_history, tiles_per_split);
+  if (partials == 0) return 0;
+  const int64_t per = requests_per_launch(num_kv_heads);
+  const int64_t reqs = num_requests < per ? num_requests : per;
+  return bounds_offset(partials) + (size_t)reqs * 2 * sizeof(int32_t);
+}
+
+int oscar_decode_only(const float* q_rot, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+                      const void* k_cache, const void* v_cache, int32_t block_size, int64_t num_pages,
+                      int64_t k_stride_page, int64_t k_stride_token, int64_t k_stride_head,
+                      int64_t v_stride_page, int64_t v_stride_token, int64_t v_stride_head,
+                      const int32_t* block_table, int64_t block_table_stride, int32_t block_table_cols,
+                      const int32_t* seq_lens, int32_t num_requests, int64_t max_history,
+                      const int64_t* stage_owner, const void* stage_k_image, const void* stage_v_image,
+                      int32_t stage_rows, int32_t sink_tokens, int32_t recent_tokens, float scale,
+                      int32_t tiles_per_split, float* out, void* workspace, size_t workspace_size,
+                      hipStream_t stream) {
+  if (head_size != kHeadDim) return kErrUnsupportedHeadDim;
+  if (num_requests < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_kv_heads > kMaxInlineItems ||
+      num_heads % num_kv_heads != 0 || max_history < 0 ||
+      block_size <= 0 || num_pages <= 0 || block_table_cols < 0 || stage_rows < 0 || sink_tokens < 0 ||
+      recent_tokens < 0 || tiles_per_split < 0 || tiles_per_split > kMaxTilesPerSplit)
+    return kErrInvalidArgument;
+  if (num_requests == 0) return kOk;
+  DecodeArgs a{};
+  int rc = fill_common(a, q_rot, num_heads, num_kv_heads, head_size, k_cache, v_cache, block_size, num_pages,
+                       k_stride_page, k_stride_token, k_stride_head, v_stride_page, v_stride_token, v_stride_head,
+                       block_table, block_table_stride, block_table_cols, max_history, stage_owner, stage_k_image,
+                       stage_v_image, stage_rows, scale, out, workspace);
+  if (rc != kOk) return rc;
+  if (!seq_lens) return kErrInvalidArgument;
+  for (int32_t i = 0; i < num_requests; ++i)
+    if (seq_lens[i] < 0 || seq_lens[i] > max_history) return kErrInvalidArgument;
+  const int tps = tiles_per_split > 0 ? tiles_per_split
+                                      : default_tiles_per_split(num_requests, num_kv_heads, max_history);
+  const int64_t splits = splits_for(max_history, tps);
+  if (splits > kMaxSplits) return kErrInvalidArgument;
+  const size_t partials = workspace_floats(num_requests, num_kv_heads, num_heads, 1, max_history, tps) *
+                          sizeof(float);
+  const int32_t per = requests_per_launch(num_kv_heads);
+  const size_t need = bounds_offset(partials) +
+                      (size_t)(num_requests < per ? num_requests : per) * 2 * sizeof(int32_t);
+  if (workspace == nullptr || workspace_size < need) return kErrWorkspaceTooSmall;
+  const bool window = stage_rows > 0;
+  int32_t* bounds = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) + bounds_offset(partials));
+  const int32_t sink_eff = window ? (sink_tokens / block_size) * block_size : 0;
+  a.k_new = nullptr;
+  a.v_new = nullptr;
+  a.win = window ? bounds : nullptr;
+  a.fresh = 0;
+  a.max_splits = (int32_t)splits;
+  a.row_tiles = (a.group + kRows - 1) / kRows;
+  if ((rc = set_split_lds()) != kOk) return rc;
+  for (int32_t c0 = 0; c0 < num_requests; c0 += per) {
+    const int32_t nreq = num_requests - c0 < per ? num_requests - c0 : per;
+    for (int32_t i = 0; i < nreq; ++i)
+      for (int32_t h = 0; h < num_kv_heads; ++h)
+        a.items[i * num_kv_heads + h] = ItemInfo{c0 + i, 1, seq_lens[c0 + i], (int16_t)i, (int16_t)h};
+    a.block_table = block_table ? block_table + (int64_t)c0 * block_table_stride : nullptr;
+    const unsigned nitems = (unsigned)(nreq * num_kv_heads);
+    if (window) {
+      hipLaunchKernelGGL(decode_only_bounds_kernel, dim3((unsigned)nreq), dim3(kBoundsThreads), 0, stream, a, bounds,
+                         sink_eff, recent_tokens);
+      if (hipGetLastError() != hipSuccess) return kErrLaunch;
+    }
+    if (a.max_splits > 0) {
+      dim3 grid((unsigned)a.max_splits, nitems, (unsigned)a.row_tiles);
+      hipLaunchKernelGGL(paged_decode_split_kernel, grid, dim3(256), kLdsBytes, stream, a);
+      if (hipGetLastError() != hipSuccess) return kErrLaunch;
+    }
     dim3 mgrid((unsigned)(kRows * 4), nitems, (unsigned)a.row_tiles);
     hipLaunchKernelGGL(paged_decode_merge_kernel, mgrid, dim3(256), 0, stream, a);
     if (hipGetLastError() != hipSuccess) return kErrLaunch;

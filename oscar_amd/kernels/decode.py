@@ -51,14 +51,34 @@ class DecodePlan:
     capturing it in a HIP graph) re-runs the same decode on the current stream.
     """
 
-    def __init__(self, args: tuple, out: torch.Tensor, keep: list):
+    def __init__(self, args: tuple, out: torch.Tensor, keep: list, entry: str = "oscar_paged_decode"):
         self.args = args
         self.out = out
         self.keep = keep
+        self.entry = entry
 
     def launch(self) -> torch.Tensor:
-        _lib.call("oscar_paged_decode", *self.args, _lib.stream_handle(self.out.device))
+        _lib.call(self.entry, *self.args, _lib.stream_handle(self.out.device))
         return self.out
+
+
+def _stage_operands(stage, bs: int, hk: int):
+    """(owner int64, k image, v image, rows) of an arena (stage_k, stage_v,
+    owner[, k_image, v_image]); the fp16 images are built when not given."""
+    owner = stage[2]
+    if owner.shape[1] != bs:
+        raise ValueError("staging arena block size must equal the cache block size")
+    owner = owner.to(torch.int64).contiguous()
+    rows = owner.shape[0]
+    if len(stage) >= 5 and stage[3] is not None:
+        kimg, vimg = stage[3], stage[4]
+    else:
+        kimg, vimg = staging.stage_images(stage[0], stage[1])
+    want = staging.image_shape(rows, bs, hk)
+    if tuple(kimg.shape) != want or tuple(vimg.shape) != want or kimg.dtype != torch.float16 \
+            or vimg.dtype != torch.float16 or not (kimg.is_contiguous() and vimg.is_contiguous()):
+        raise ValueError(f"staging operand images must be contiguous fp16 {want}")
+    return owner, kimg, vimg, rows
 
 
 def plan(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None, out=None,
@@ -86,19 +106,7 @@ def plan(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None, out=None,
     seq_t = (ctypes.c_int32 * max(len(seqs), 1))(*[int(x) for x in seqs])
     bs, pages, kst, vst = cache_geometry(kc, vc)
     if stage is not None:
-        owner = stage[2]
-        if owner.shape[1] != bs:
-            raise ValueError("staging arena block size must equal the cache block size")
-        owner = owner.to(torch.int64).contiguous()
-        rows = owner.shape[0]
-        if len(stage) >= 5 and stage[3] is not None:
-            kimg, vimg = stage[3], stage[4]
-        else:
-            kimg, vimg = staging.stage_images(stage[0], stage[1])
-        want = staging.image_shape(rows, bs, hk)
-        if tuple(kimg.shape) != want or tuple(vimg.shape) != want or kimg.dtype != torch.float16 \
-                or vimg.dtype != torch.float16 or not (kimg.is_contiguous() and vimg.is_contiguous()):
-            raise ValueError(f"staging operand images must be contiguous fp16 {want}")
+        owner, kimg, vimg, rows = _stage_operands(stage, bs, hk)
     else:
         owner = kimg = vimg = None
         rows = 0
@@ -121,3 +129,48 @@ def paged_attention(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None) ->
     if q.shape[0] == 0:
         return torch.empty(q.shape, dtype=torch.float32, device=q.device)
     return plan(q, k, v, kc, vc, bt, qsl, seqs, scale, stage).launch()
+
+
+def decode_only_plan(q, kc, vc, bt, seqs, scale: float, stage=None, sink_tokens: int = 0,
+                     recent_tokens: int = 0, out=None, tiles_per_split: int = 0) -> DecodePlan:
+    """The DecodeOnly read (backend.py:321-358, 500-611): one rotated query
+    per request [B, Hq, D] over its whole history [0, seqs[i]); with a window
+    arena, staged values only in the reference's windowed segments (the sink
+    when fully staged, the staged run ending at seq - 1 inside the recent
+    window).  ``seqs`` is a host list; returns fp32 [B, Hq, D] rotated-V."""
+    B, hq, d = q.shape
+    check_d(d)
+    if len(seqs) != B or any(s < 0 for s in seqs):
+        raise ValueError("DecodeOnly needs one query token and a non-negative length per request")
+    if bt.ndim != 2 or bt.shape[0] < B:
+        raise ValueError("block table must be [requests, pages]")
+    dev = q.device
+    q = q.float().contiguous()
+    bt = bt.to(device=dev, dtype=torch.int32).contiguous()
+    seq_t = (ctypes.c_int32 * max(B, 1))(*[int(x) for x in seqs])
+    max_hist = max(seqs, default=0)
+    bs, pages, kst, vst = cache_geometry(kc, vc)
+    hk = kc.shape[2]
+    if bs % 32:
+        raise ValueError("paged decode needs a cache block size that is a multiple of 32")
+    owner = kimg = vimg = None
+    rows = 0
+    if stage is not None:
+        owner, kimg, vimg, rows = _stage_operands(stage, bs, hk)
+    need = _lib.load().oscar_decode_only_workspace_bytes(B, hk, hq, max_hist, tiles_per_split)
+    ws = workspace(dev, need)
+    if out is None:
+        out = torch.empty(B, hq, d, dtype=torch.float32, device=dev)
+    args = (_lib.ptr(q), hq, hk, d, _lib.ptr(kc), _lib.ptr(vc), bs, pages, *kst, *vst, _lib.ptr(bt),
+            bt.stride(0), bt.shape[1], ctypes.addressof(seq_t), B, max_hist, _lib.ptr(owner), _lib.ptr(kimg),
+            _lib.ptr(vimg), rows, int(sink_tokens), int(recent_tokens), float(scale), int(tiles_per_split),
+            _lib.ptr(out), _lib.ptr(ws), ws.numel())
+    return DecodePlan(args, out, [q, kc, vc, bt, seq_t, owner, kimg, vimg, ws], entry="oscar_decode_only")
+
+
+def decode_only(q, kc, vc, bt, seqs, scale: float, stage=None, sink_tokens: int = 0,
+                recent_tokens: int = 0) -> torch.Tensor:
+    """Rotated-domain DecodeOnly attention; returns fp32 [B, Hq, D]."""
+    if q.shape[0] == 0:
+        return torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    return decode_only_plan(q, kc, vc, bt, seqs, scale, stage, sink_tokens, recent_tokens).launch()

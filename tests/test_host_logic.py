@@ -215,6 +215,26 @@ def test_forward_without_metadata_zeroes_output(clean_env):
     assert torch.count_nonzero(impl.forward(NS(layer_name="l.0"), out, out, out, caches, None, output=out)) == 0
 
 
+def test_forward_without_fresh_kv_needs_the_decode_only_state(clean_env):
+    """backend.py:304-309: key = None reads only in the DecodeOnly state, one
+    query token per request (checked before any kernel call)."""
+    from oscar_amd.backend import OscarAttentionState
+
+    impl = make_impl(clean_env)
+    caches = [torch.zeros(2, 128, 1, 256, dtype=torch.int8) for _ in range(2)]
+    out = torch.zeros(2, 6, 256)
+    md = NS(num_actual_tokens=2, query_start_loc=torch.tensor([0, 2]), seq_lens=torch.tensor([9]),
+            seq_lens_list=[9], block_tables=torch.zeros(1, 2, dtype=torch.int32))
+    with pytest.raises(NotImplementedError):
+        impl.forward(NS(layer_name="l.0"), out, None, None, caches, md, output=out)
+    md.attn_state = OscarAttentionState.ChunkedPrefill
+    with pytest.raises(NotImplementedError):
+        impl.forward(NS(layer_name="l.0"), out, None, None, caches, md, output=out)
+    md.attn_state = OscarAttentionState.DecodeOnly
+    with pytest.raises(ValueError, match="one query token"):
+        impl.forward(NS(layer_name="l.0"), out, None, None, caches, md, output=out)
+
+
 # ---------------------------------------------------------------- budgeting
 def test_budget_accounts_shadow_and_fixed_buffers():
     budget = integration.memory_budget(10000, 100, 25, 1000)
