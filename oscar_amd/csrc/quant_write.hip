@@ -390,17 +390,20 @@ __global__ __launch_bounds__(256, 2) void quant_write_fused_kernel(
   const bool live = tok < n_tokens;
   const uint8_t* rop = side == 0 ? rot_k : rot_v;
 
-  // B operand: this lane's token, input features 128*half + 8m .. +7 for m = 0..15.
-  bf16x8 xb[16];
-  {
-    const uint16_t* src = (side == 0 ? key : value) + (live ? tok : 0) * token_stride +
-                          (int64_t)head * kHeadDim + half * kPerLane;
+  // B operand of K step m: this lane's token, input features 128*half + 8m .. +7.
+  // Loaded in two halves, each one 128-byte line of the lane's half-row:
+  // steps 0..7 up front, steps 8..15 during step 4, so the first step waits
+  // for half the loads and each line is still fetched in one burst.
+  const uint16_t* xsrc = (side == 0 ? key : value) + (live ? tok : 0) * token_stride +
+                         (int64_t)head * kHeadDim + half * kPerLane;
+  // A lane past the last token reads token 0: its MFMA column (and the
+  // vector the selection then computes) is never stored.
+  auto load_x = [&](int m) -> bf16x8 {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(xsrc + 8 * m));
+  };
+  bf16x8 xlo[8], xhi[8];
 #pragma unroll
-    for (int m = 0; m < 16; ++m) {
-      u32x4 raw = live ? *reinterpret_cast<const u32x4*>(src + 8 * m) : u32x4{0u, 0u, 0u, 0u};
-      xb[m] = __builtin_bit_cast(bf16x8, raw);
-    }
-  }
+  for (int m = 0; m < 8; ++m) xlo[m] = load_x(m);
   // Thread's share of a chunk: wave w copies 1 KB blocks 4w .. 4w + 3.
   auto request = [&](int chunk) {
 #pragma unroll
@@ -420,14 +423,22 @@ __global__ __launch_bounds__(256, 2) void quant_write_fused_kernel(
 
 #pragma unroll
   for (int m = 0; m < kSteps; ++m) {
-    // This thread's copies of chunk m have landed (later chunks may still be
-    // in flight); after the barrier every thread's have, and chunk m - 1's
-    // slot is free for chunk m + 3.
-    if (m + 2 < kSteps) wait_vmcnt<2 * kDmaPerChunk>();
+    // This thread's copies of chunk m (and x_m) have landed (later ones may
+    // still be in flight); after the barrier every thread's have, and chunk
+    // m - 1's slot is free for chunk m + 3.  Issue order: x_0..7, chunks
+    // 0..2, then per step chunk m + 3, and x_8..15 after chunk 7 (step 4);
+    // what was issued after chunk m is left outstanding.
+    if (m >= 5 && m <= 7) wait_vmcnt<2 * kDmaPerChunk + 8>();
+    else if (m + 2 < kSteps) wait_vmcnt<2 * kDmaPerChunk>();
     else if (m + 1 < kSteps) wait_vmcnt<kDmaPerChunk>();
     else wait_vmcnt<0>();
     lds_barrier();
     if (m + 3 < kSteps) request(m + 3);
+    if (m == 4) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) xhi[k] = load_x(8 + k);
+    }
+    const bf16x8 xm = m < 8 ? xlo[m] : xhi[m - 8];
     const u32x4* a_src = reinterpret_cast<const u32x4*>(ring + (m % kRing) * kChunkBytes);
     // Operand reads run kAhead MFMAs ahead of their use (register rotation);
     // the 8 tiles' hi passes come first, then their lo passes.
@@ -439,7 +450,7 @@ __global__ __launch_bounds__(256, 2) void quant_write_fused_kernel(
     for (int i = 0; i < 16; ++i) {
       const bf16x8 cur = a[i % kAhead];
       if (i + kAhead < 16) a[i % kAhead] = __builtin_bit_cast(bf16x8, a_src[(i + kAhead) * 64 + lane]);
-      acc[i & 7] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur, xb[m], acc[i & 7], 0, 0, 0);
+      acc[i & 7] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur, xm, acc[i & 7], 0, 0, 0);
     }
     // Keep that pipeline in the schedule: kAhead LDS reads, then each MFMA
     // followed by the read kAhead positions ahead.
