@@ -121,3 +121,11 @@ def impl_block_table(olayer, pool, seed):
     perm = synthetic.page_permutation(pool, seed + 2)
     per = pool // 2
     return torch.stack([perm[i * per:(i + 1) * per] for i in range(2)])
+
+
+@pytest.mark.parametrize("cache_dtype", [torch.int8, torch.bfloat16])
+def test_four_kv_heads_and_both_cache_geometries(device, cache_dtype):
+    hist = [1500, 70, 640]
+    case = decode_case(hist, [1] * len(hist), bs=64, seed=47, hk=4, hq=8, sink=64, recent=128, staging=1024,
+                       cache_dtype=cache_dtype)
+    run_case(case, device, plant=[(2, case.seqs[2] - 3)])
