@@ -37,13 +37,16 @@ class Engine:
 
     def __init__(self, device, layer_ids=(0,), layer_types=("full_attention", "linear_attention"),
                  block_size=32, blocks=8, free_bytes=200 * 10 ** 6, num_kv_heads=1, num_heads=6,
-                 window=True, tp=1, overrides=None):
+                 window=True, tp=1, overrides=None, modules=None):
+        """modules: {layer name: attention module} built elsewhere (by the
+        plugin, say) to use instead of fresh OSCAR layers."""
         self.device = torch.device(device)
         self.block_size, self.blocks = block_size, blocks
         self.layers = {}
-        for i in layer_ids:
+        for i in layer_ids if modules is None else ():
             name = f"model.layers.{i}.self_attn.attn"
             self.layers[name] = NS(layer_name=name, impl=make_impl(num_kv_heads, num_heads, window=window))
+        self.layers.update(modules or {})
         self.native_name = "model.layers.99.linear_attn"
         ctx = dict(self.layers)
         ctx[self.native_name] = NS(layer_name=self.native_name, impl=NS())
@@ -91,6 +94,17 @@ class Engine:
 
         self.Runner, self.Worker = GPUModelRunner, Worker
         self.groups_calls = []
+        self._ctx, self._heads = ctx, num_kv_heads
+
+    def add_module(self, module):
+        """Register one more attention module (e.g. built by the plugin after
+        the fake worker modules were installed)."""
+        self.layers[module.layer_name] = module
+        self._ctx[module.layer_name] = module
+        self.specs[module.layer_name] = NS(block_size=self.block_size, num_kv_heads=self._heads, head_size=HEAD,
+                                           head_size_v=HEAD)
+        self.block_bytes = 2 * self.block_size * self._heads * HEAD * len(self._ctx)
+        self.provisional = NS(kv_cache_tensors=[NS(size=self.block_bytes * self.blocks)], num_blocks=self.blocks)
 
     def modules(self):
         engine = self
