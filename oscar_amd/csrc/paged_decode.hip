@@ -382,7 +382,12 @@ __device__ __forceinline__ T pick4(T v0, T v1, T v2, T v3, int i) {
 
 __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
-  const int split = blockIdx.x;
+  // History splits are dispatched as 0, S - 1, S - 2, ..., 1: the first and
+  // last steps hold the window tokens, whose extra passes make them the
+  // longest workgroups, so they start first (measured: C5 decode 37.6 ->
+  // 34 us, C2 unchanged).
+  const int bx = blockIdx.x;
+  const int split = bx >= a.max_splits ? bx : (bx == 0 ? 0 : a.max_splits - bx);
   const int item = blockIdx.y;
   const int rt = blockIdx.z;
   const ItemInfo it = a.items[item];
