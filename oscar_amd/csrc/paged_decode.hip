@@ -917,6 +917,59 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
   }
 }
 
+// Merge for launches with few partials per item (at most kSmallP, e.g. many
+// requests with a handful of splits each): one thread per four features of a
+// row loads every partial's slice and (m, l) itself, so the combine needs no
+// LDS round.  256 threads = 16 row-quarters x 16 threads.
+constexpr int kSmallP = 32;
+
+__global__ __launch_bounds__(256) void paged_decode_merge_small_kernel(DecodeArgs a) {
+  const int tid = threadIdx.x;
+  const int rq = blockIdx.x * 16 + (tid >> 4);
+  const int r = rq >> 2, qd = rq & 3;
+  const int item = blockIdx.y;
+  const int rt = blockIdx.z;
+  const ItemInfo it = a.items[item];
+  const int rows = it.nq * a.group;
+  const int row = rt * kRows + r;
+  if (it.nq <= 0 || r >= kRows || row >= rows) return;
+  const int steps = (it.prefix + kStepTok - 1) / kStepTok;
+  const int hs = min(a.max_splits, steps);
+  const int P = hs + a.fresh;
+  const float* base = a.ws + item_index(a, item, 0, rt) * kPartialFloats;
+  const int64_t pstride = (int64_t)a.row_tiles * kPartialFloats;
+  const int f0 = 64 * qd + 4 * (tid & 15);
+  float m[kSmallP], l[kSmallP];
+  floatx4 x[kSmallP];
+#pragma unroll
+  for (int p = 0; p < kSmallP; ++p) {
+    m[p] = -__builtin_inff();
+    l[p] = 0.f;
+    x[p] = floatx4{};
+    if (p < P) {
+      const float* pp = base + (p < hs ? p : a.max_splits) * pstride;
+      m[p] = pp[kPartO + r];
+      l[p] = pp[kPartO + kRows + r];
+      x[p] = *reinterpret_cast<const floatx4*>(pp + r * kHeadDim + f0);
+    }
+  }
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int p = 0; p < kSmallP; ++p) mx = fmaxf(mx, m[p]);
+  floatx4 acc = floatx4{};
+  float ls = 0.f;
+#pragma unroll
+  for (int p = 0; p < kSmallP; ++p) {
+    const float wgt = (m[p] == -__builtin_inff()) ? 0.f : exp2f(m[p] - mx);
+    acc += wgt * x[p];
+    ls = fmaf(wgt, l[p], ls);
+  }
+  const int j = row / a.group;
+  const int h = it.kvh * a.group + (row - j * a.group);
+  const float inv = ls > 0.f ? 1.f / ls : 0.f;
+  *reinterpret_cast<floatx4*>(a.out + ((int64_t)(it.qa + j) * a.num_heads + h) * kHeadDim + f0) = acc * inv;
+}
+
 // DecodeOnly window bounds of the launch chunk's requests (backend.py:514-551):
 // win[2r] = head (sink_eff when the request is longer than the sink and every
 // seat of its sink pages holds that page, else 0), win[2r + 1] = cut (start of
@@ -1076,6 +1129,24 @@ int set_split_lds() {
   return kOk;
 }
 
+// Merge blocks per feature quarter: one per row of a row tile that can hold
+// rows (a launch's longest request fills at most this many).
+int merge_rows(int64_t rows) { return (int)(rows < kRows ? rows : kRows); }
+
+// The merge of one launch chunk: the per-thread combine when every item has
+// at most kSmallP partials, else one block per (row, feature quarter).
+int launch_merge(const DecodeArgs& a, int64_t max_rows, unsigned nitems, hipStream_t stream) {
+  const int mr = merge_rows(max_rows);
+  if (a.max_splits + a.fresh <= kSmallP) {
+    dim3 grid((unsigned)((mr * 4 + 15) / 16), nitems, (unsigned)a.row_tiles);
+    hipLaunchKernelGGL(paged_decode_merge_small_kernel, grid, dim3(256), 0, stream, a);
+  } else {
+    dim3 grid((unsigned)(mr * 4), nitems, (unsigned)a.row_tiles);
+    hipLaunchKernelGGL(paged_decode_merge_kernel, grid, dim3(256), 0, stream, a);
+  }
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
 // Bytes of the DecodeOnly bounds array after the partials (256-byte aligned).
 size_t bounds_offset(size_t partial_bytes) { return (partial_bytes + 255) & ~(size_t)255; }
 
@@ -1163,9 +1234,7 @@ int oscar_paged_decode(const float* q_rot, const float* k_new, const float* v_ne
     dim3 grid((unsigned)(a.max_splits + 1), nitems, (unsigned)a.row_tiles);
     hipLaunchKernelGGL(paged_decode_split_kernel, grid, dim3(256), kLdsBytes, stream, a);
     if (hipGetLastError() != hipSuccess) return kErrLaunch;
-    dim3 mgrid((unsigned)(kRows * 4), nitems, (unsigned)a.row_tiles);
-    hipLaunchKernelGGL(paged_decode_merge_kernel, mgrid, dim3(256), 0, stream, a);
-    if (hipGetLastError() != hipSuccess) return kErrLaunch;
+    if ((rc = launch_merge(a, (int64_t)max_query_len * a.group, nitems, stream)) != kOk) return rc;
   }
   return kOk;
 }
@@ -1243,9 +1312,7 @@ int oscar_decode_only(const float* q_rot, int32_t num_heads, int32_t num_kv_head
       hipLaunchKernelGGL(paged_decode_split_kernel, grid, dim3(256), kLdsBytes, stream, a);
       if (hipGetLastError() != hipSuccess) return kErrLaunch;
     }
-    dim3 mgrid((unsigned)(kRows * 4), nitems, (unsigned)a.row_tiles);
-    hipLaunchKernelGGL(paged_decode_merge_kernel, mgrid, dim3(256), 0, stream, a);
-    if (hipGetLastError() != hipSuccess) return kErrLaunch;
+    if ((rc = launch_merge(a, a.group, nitems, stream)) != kOk) return rc;
   }
   return kOk;
 }
