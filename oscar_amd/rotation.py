@@ -1,107 +1,116 @@
-"""Per-layer orthogonal K/V rotations.
+"""Per-layer orthogonal K/V rotations read from a checkpoint file.
 
-Same checkpoint formats and lookup rules as the reference loader
-(oscar_ascend/rotation.py:18-129):
-  * ``{"layers": {id: {"rotation": R_k, "rotation_v": R_v, ...}}}``
-    (ids may be ints, numeric strings or module names),
-  * ``{id: R}`` or ``{id: {"rotation": ...}}``,
-  * a stacked ``[num_layers, D, D]`` tensor.
-An empty path gives the identity; a missing layer gives the identity unless
-``strict`` (then ValueError); strict mode also rejects non-finite or
-non-orthogonal matrices.  Files are read with ``weights_only=True``.
+Checkpoint layouts accepted (the on-disk formats of the reference's loader,
+oscar_ascend/rotation.py:44-90, and of the calibration tool's output):
+
+  1. {"layers": {layer_id: entry}, ...}      calibration output (format v2
+     adds "format_version": 2 and an "objective" naming "r_h_pbr");
+  2. {layer_id: entry}                       a bare mapping;
+  3. a tensor [num_layers, D, D]             layer i is slice i.
+
+An entry is a [D, D] tensor (the K rotation) or a dict holding "rotation"
+(and optionally "rotation_v" and other tensors).  A layer_id is an int, a
+numeric string or a module name; module names and vLLM layer names map to an
+index by their ".layers.<i>." component, else by their last integer.
+
+Lookup: an empty path or an absent layer gives the identity (strict mode:
+ValueError for an absent layer, and for a matrix that is not finite or not
+orthogonal within 1e-3).  The V rotation is "rotation_v" when the entry has
+one, else "rotation".  Files are read with ``weights_only=True``: a
+checkpoint that needs unpickling of arbitrary objects is refused.
 """
 from __future__ import annotations
 
 import re
+import warnings
 from functools import lru_cache
 
 import torch
 
-_LAYER_RE = re.compile(r"\.layers\.(\d+)\.")
+_DECODER_INDEX = re.compile(r"\.layers\.(\d+)\.")
+_DIGITS = re.compile(r"\d+")
 
 
-def layer_index_from_name(layer_name: str) -> int | None:
-    """rotation.py:18-24 — '.layers.<i>.' first, else the last integer in the name."""
-    m = _LAYER_RE.search(layer_name)
-    if m is not None:
-        return int(m.group(1))
-    ints = re.findall(r"\d+", layer_name)
-    return int(ints[-1]) if ints else None
+def layer_index_from_name(name: str) -> int | None:
+    """Decoder-layer index of a module or layer name (None if it has no digits)."""
+    found = _DECODER_INDEX.search(name)
+    if found:
+        return int(found.group(1))
+    runs = _DIGITS.findall(name)
+    return int(runs[-1]) if runs else None
 
 
-def _resolve_key(key) -> int | None:
-    """rotation.py:28-41 — int, numeric string or module-name keys."""
+def _layer_id(key) -> int | None:
     if isinstance(key, int):
         return key
     if isinstance(key, str):
-        try:
-            return int(key)
-        except ValueError:
-            return layer_index_from_name(key)
+        return int(key) if key.strip().lstrip("+-").isdigit() else layer_index_from_name(key)
     return None
 
 
-def _tensors(entry: dict) -> dict:
-    return {k: v.float().contiguous() for k, v in entry.items() if isinstance(v, torch.Tensor)}
+def _as_entry(value, where: str) -> dict[str, torch.Tensor]:
+    if isinstance(value, torch.Tensor):
+        return {"rotation": value.float().contiguous()}
+    if isinstance(value, dict) and isinstance(value.get("rotation"), torch.Tensor):
+        return {k: t.float().contiguous() for k, t in value.items() if isinstance(t, torch.Tensor)}
+    raise ValueError(f"{where}: a layer entry must be a matrix or hold a 'rotation' matrix")
+
+
+def _is_v2_recipe(obj) -> bool:
+    return isinstance(obj, dict) and obj.get("format_version", 0) >= 2 and "r_h_pbr" in str(obj.get("objective", ""))
 
 
 @lru_cache(maxsize=8)
-def load_checkpoint(path: str) -> dict:
-    """rotation.py:44-90 — {layer id: {"rotation": R_k, ["rotation_v": R_v]}}."""
+def load_checkpoint(path: str) -> dict[int, dict[str, torch.Tensor]]:
+    """{layer index: {"rotation": R_k[, "rotation_v": R_v, ...]}} of one file (cached)."""
     obj = torch.load(path, map_location="cpu", weights_only=True)
-    if not (isinstance(obj, dict) and obj.get("format_version", 0) >= 2
-            and "r_h_pbr" in str(obj.get("objective", ""))):
-        print(f"[oscar-amd] rotation checkpoint {path!r} is not a v2 (U@H@P_br) recipe; "
-              "per-vector INT2 accuracy will suffer")
-    table: dict[int, dict] = {}
-    if isinstance(obj, dict) and "layers" in obj:
-        for key, entry in obj["layers"].items():
-            lid = _resolve_key(key)
-            if lid is None:
-                continue
-            if isinstance(entry, dict) and "rotation" in entry:
-                table[lid] = _tensors(entry)
-            else:
-                table[lid] = {"rotation": entry.float().contiguous()}
-    elif isinstance(obj, dict):
-        for key, entry in obj.items():
-            lid = _resolve_key(key)
-            if lid is None:
-                continue
-            if isinstance(entry, dict) and "rotation" in entry:
-                table[lid] = _tensors(entry)
-            elif isinstance(entry, torch.Tensor):
-                table[lid] = {"rotation": entry.float().contiguous()}
-    elif torch.is_tensor(obj) and obj.dim() == 3:
-        for lid in range(obj.shape[0]):
-            table[lid] = {"rotation": obj[lid].float().contiguous()}
-    else:
-        raise ValueError(f"Unrecognized OSCAR rotation checkpoint structure at {path!r}: {type(obj)}")
+    if not _is_v2_recipe(obj):
+        warnings.warn(f"OSCAR rotations in {path} are not a format-v2 U@H@P_br calibration; "
+                      "per-vector INT2 error will be higher than calibrated", stacklevel=2)
+    if torch.is_tensor(obj):
+        if obj.dim() != 3:
+            raise ValueError(f"{path}: a stacked rotation tensor must be [layers, D, D], got {tuple(obj.shape)}")
+        return {i: {"rotation": obj[i].float().contiguous()} for i in range(obj.shape[0])}
+    if not isinstance(obj, dict):
+        raise ValueError(f"{path}: expected a mapping or a stacked tensor of rotations, found {type(obj).__name__}")
+    layers = obj["layers"] if "layers" in obj else obj
+    table = {}
+    for key, value in layers.items():
+        lid = _layer_id(key)
+        if lid is None:
+            continue                 # metadata keys such as "format_version"
+        if "layers" not in obj and not isinstance(value, (torch.Tensor, dict)):
+            continue
+        table[lid] = _as_entry(value, f"{path} [{key!r}]")
     return table
+
+
+def _check_orthogonal(R: torch.Tensor, where: str) -> None:
+    if not torch.isfinite(R).all():
+        raise ValueError(f"{where}: rotation holds non-finite values")
+    gram = R @ R.t()
+    if not torch.allclose(gram, torch.eye(R.shape[0]), atol=1e-3, rtol=1e-3):
+        dev = (gram - torch.eye(R.shape[0])).abs().max().item()
+        raise ValueError(f"{where}: rotation is not orthogonal (max |R R^T - I| = {dev:.2e})")
 
 
 def get_layer_rotation(path: str, layer_name: str, head_dim: int, device, dtype=torch.float32,
                        mode: str = "k", strict: bool = False) -> torch.Tensor:
-    """rotation.py:93-129 — this layer's [D, D] rotation (mode 'v' prefers rotation_v)."""
+    """The [D, D] rotation of one layer (x_rot = x @ R); mode "v" prefers rotation_v."""
+    eye = lambda: torch.eye(head_dim, device=device, dtype=dtype)  # noqa: E731
     if not path:
-        return torch.eye(head_dim, device=device, dtype=dtype)
-    table = load_checkpoint(path)
+        return eye()
     lid = layer_index_from_name(layer_name)
-    entry = table.get(lid) if lid is not None else None
+    entry = load_checkpoint(path).get(lid) if lid is not None else None
     if entry is None:
         if strict:
-            raise ValueError(f"Rotation checkpoint {path!r} is missing layer {layer_name}")
-        return torch.eye(head_dim, device=device, dtype=dtype)
-    rot = entry.get("rotation_v") if mode == "v" else entry.get("rotation")
-    if rot is None:
-        rot = entry.get("rotation")
-    if rot is None:
-        return torch.eye(head_dim, device=device, dtype=dtype)
-    if rot.shape != (head_dim, head_dim):
-        raise ValueError(f"OSCAR rotation for layer {lid} has shape {tuple(rot.shape)}, "
-                         f"expected ({head_dim}, {head_dim}).")
+            raise ValueError(f"{path} has no rotation for layer {layer_name!r} (index {lid})")
+        return eye()
+    R = entry.get("rotation_v") if mode == "v" else None
+    R = entry["rotation"] if R is None else R
+    where = f"{path} layer {lid} ({mode})"
+    if tuple(R.shape) != (head_dim, head_dim):
+        raise ValueError(f"{where}: rotation shape {tuple(R.shape)} does not match head_dim {head_dim}")
     if strict:
-        eye = torch.eye(head_dim)
-        if not torch.isfinite(rot).all() or not torch.allclose(rot @ rot.t(), eye, atol=1e-3, rtol=1e-3):
-            raise ValueError(f"Rotation checkpoint {path!r} layer {lid} is not finite/orthogonal")
-    return rot.to(device=device, dtype=dtype).contiguous()
+        _check_orthogonal(R, where)
+    return R.to(device=device, dtype=dtype).contiguous()

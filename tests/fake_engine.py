@@ -7,6 +7,7 @@ whose profiler reports a fixed number of free bytes, and an engine allocator
 that hands each layer its (K, V) cache pair."""
 from __future__ import annotations
 
+import dataclasses
 import sys
 from types import ModuleType
 from types import SimpleNamespace as NS
@@ -24,9 +25,8 @@ def make_impl(num_kv_heads=1, num_heads=6, sink=64, recent=64, staging=256, wind
     impl.scale = HEAD ** -0.5
     impl.key_cache = impl.value_cache = None
     impl._oscar_setup()
-    cfg = impl._oscar
-    cfg.sink_tokens, cfg.recent_tokens, cfg.staging_tokens = sink, recent, staging
-    cfg.window_enabled = window
+    impl._oscar_cfg = dataclasses.replace(impl._oscar, sink_tokens=sink, recent_tokens=recent,
+                                          staging_tokens=staging if window else 0)
     return impl
 
 

@@ -15,6 +15,7 @@ U @ H @ P_br.  The whole tool runs once against a fake vLLM engine.
 import json
 import sys
 from types import ModuleType
+import warnings
 from types import SimpleNamespace as NS
 
 import pytest
@@ -180,16 +181,16 @@ def test_checkpoint_round_trip_through_the_loader(tmp_path, capsys):
     path = tmp_path / "rot.pt"
     torch.save(ckpt, path)
     rotation.load_checkpoint.cache_clear()
-    capsys.readouterr()
-    for lid in (3, 7):
-        name = f"model.layers.{lid}.self_attn.attn"
-        rk = rotation.get_layer_rotation(str(path), name, D, "cpu", mode="k", strict=True)
-        rv = rotation.get_layer_rotation(str(path), name, D, "cpu", mode="v", strict=True)
-        assert torch.equal(rk, ckpt["layers"][str(lid)]["rotation"])
-        assert torch.equal(rv, ckpt["layers"][str(lid)]["rotation_v"])
-        assert not torch.equal(rk, rv)
-    assert "not a v2" not in capsys.readouterr().out
-    with pytest.raises(ValueError, match="missing layer"):
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")          # a format-v2 checkpoint loads without the recipe warning
+        for lid in (3, 7):
+            name = f"model.layers.{lid}.self_attn.attn"
+            rk = rotation.get_layer_rotation(str(path), name, D, "cpu", mode="k", strict=True)
+            rv = rotation.get_layer_rotation(str(path), name, D, "cpu", mode="v", strict=True)
+            assert torch.equal(rk, ckpt["layers"][str(lid)]["rotation"])
+            assert torch.equal(rv, ckpt["layers"][str(lid)]["rotation_v"])
+            assert not torch.equal(rk, rv)
+    with pytest.raises(ValueError, match="has no rotation for layer"):
         rotation.get_layer_rotation(str(path), "model.layers.0.self_attn.attn", D, "cpu", strict=True)
     rotation.load_checkpoint.cache_clear()
     with pytest.raises(ValueError):

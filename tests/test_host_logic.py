@@ -8,6 +8,7 @@ read of query starts), 135-149 (failed surgery restores class and state),
 tests/test_numeric.py:172-182, 216-244, 274-296, 369-378, 441-486.
 """
 import os
+import warnings
 from types import SimpleNamespace as NS
 
 import pytest
@@ -64,6 +65,23 @@ def test_layer_index_from_name():
     assert rotation.layer_index_from_name("attn") is None
 
 
+NOT_V2 = "ignore:OSCAR rotations in .* are not a format-v2"
+
+
+def test_rotation_loader_warns_on_non_v2_recipes(tmp_path):
+    p = tmp_path / "plain.pt"
+    torch.save({"layers": {"0": {"rotation": torch.eye(8)}}}, p)
+    rotation.load_checkpoint.cache_clear()
+    with pytest.warns(UserWarning, match="not a format-v2"):
+        rotation.get_layer_rotation(str(p), "model.layers.0.a", 8, "cpu")
+    p2 = tmp_path / "v2.pt"
+    torch.save({"format_version": 2, "objective": "qqt+sst r_h_pbr", "layers": {"0": {"rotation": torch.eye(8)}}}, p2)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        rotation.get_layer_rotation(str(p2), "model.layers.0.a", 8, "cpu")
+
+
+@pytest.mark.filterwarnings(NOT_V2)
 def test_rotation_checkpoint_formats(tmp_path):
     g = torch.Generator().manual_seed(0)
     R1, R2, R3 = (torch.linalg.qr(torch.randn(64, 64, generator=g)).Q for _ in range(3))
@@ -85,11 +103,12 @@ def test_rotation_checkpoint_formats(tmp_path):
     assert torch.equal(rotation.get_layer_rotation("", name, 64, "cpu"), torch.eye(64))
 
 
+@pytest.mark.filterwarnings(NOT_V2)
 def test_rotation_strict_mode(tmp_path):
     p = tmp_path / "r.pt"
     torch.save({"layers": {"1": {"rotation": torch.eye(64)}, "2": {"rotation": 2 * torch.eye(64)},
                            "5": {"rotation": torch.eye(32)}}}, p)
-    with pytest.raises(ValueError, match="missing layer"):
+    with pytest.raises(ValueError, match="has no rotation for layer"):
         rotation.get_layer_rotation(str(p), "model.layers.0.self_attn.attn", 64, "cpu", strict=True)
     with pytest.raises(ValueError, match="orthogonal"):
         rotation.get_layer_rotation(str(p), "model.layers.2.self_attn.attn", 64, "cpu", strict=True)
@@ -97,6 +116,7 @@ def test_rotation_strict_mode(tmp_path):
         rotation.get_layer_rotation(str(p), "model.layers.5.self_attn.attn", 64, "cpu")
 
 
+@pytest.mark.filterwarnings(NOT_V2)
 def test_rotation_loader_refuses_pickled_objects(tmp_path):
     p = tmp_path / "evil.pt"
     torch.save({"layers": {"1": {"rotation": torch.eye(4), "obj": NS(x=1)}}}, p)
