@@ -123,6 +123,29 @@ int oscar_paged_decode(const float* q_rot, const float* k_new, const float* v_ne
                        int32_t tiles_per_split, float* out, void* workspace,
                        size_t workspace_size, oscar_stream_t stream);
 
+/* Same decode with the reference's output rotation and cast fused into the
+ * merge: out = (attention in the rotated-V domain) @ R_v^T, written as fp32
+ * (out_bf16 = 0) or bf16 round-to-nearest-even (out_bf16 = 1) at
+ * out[token * out_token_stride + head * D + feature].  Replaces the
+ * `.float() @ R_vT` and `.to(query.dtype)` after oscar_paged_attention_triton
+ * (oscar_ascend/backend.py:291-295, 313-317).  rot_v_t: R_v^T fp32 [D][D]
+ * row-major; other arguments and the workspace as oscar_paged_decode.
+ */
+int oscar_paged_decode_rotated(const float* q_rot, const float* k_new, const float* v_new,
+                               int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                               int32_t head_size, const void* k_cache, const void* v_cache,
+                               int32_t block_size, int64_t num_pages, int64_t k_stride_page,
+                               int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
+                               int64_t v_stride_token, int64_t v_stride_head, const int32_t* block_table,
+                               int64_t block_table_stride, int32_t block_table_cols,
+                               const int32_t* query_start_loc, const int32_t* seq_lens,
+                               int32_t num_requests, int32_t max_query_len, int64_t max_history,
+                               const int64_t* stage_owner, const void* stage_k_image,
+                               const void* stage_v_image, int32_t stage_rows, float scale,
+                               int32_t tiles_per_split, const float* rot_v_t, void* out,
+                               int64_t out_token_stride, int32_t out_bf16, void* workspace,
+                               size_t workspace_size, oscar_stream_t stream);
+
 /* ---------------------------------------------------------------- DecodeOnly decode
  * One query token per request over its whole history [0, seq_lens[i]) when
  * the step brings no fresh K/V (key = None).  Replaces
@@ -176,6 +199,35 @@ int oscar_prefill_continuation(const float* q_rot, const float* k_new, const flo
                                int64_t cached_len, const float* stage_k, const float* stage_v,
                                const int64_t* stage_owner, int32_t stage_rows, float scale,
                                float* out, oscar_stream_t stream);
+
+/* ---------------------------------------------------------------- step write
+ * Everything a short step (num_tokens <= 1024 new tokens, e.g. MTP decode)
+ * writes, in one launch: q_rot = query @ R_k, k_rot = key @ R_k, v_rot =
+ * value @ R_v (fp32, the read kernels' inputs), the INT2 write of k_rot /
+ * v_rot (clip, quantize, pack, slot write; bytes as oscar_quant_write) and,
+ * with an arena (stage_rows > 0), the window write of oscar_staging_write
+ * (same seat, winner and keep rules; the arena's fp16 operand images are
+ * refreshed when given).  Replaces do_kv_cache_update + _staging_write + the
+ * q/k/v rotations of the paged read (oscar_ascend/backend.py:150-189,
+ * 261-269, 291-295, 439-481) for such steps.
+ *   query_bf16 [num_tokens][query_token_stride], key_bf16 / value_bf16
+ *     [num_tokens][kv_token_stride] (the Hk * D features of each token first);
+ *   rot_k / rot_v fp32 [D][D] (x_rot = x @ R);
+ *   query_start_loc [num_requests + 1], seq_lens [num_requests] in HOST memory
+ *     (token t of request i sits at seq_lens[i] - query_start_loc[i + 1] + t);
+ *   q_rot [num_tokens][Hq][D], k_rot / v_rot [num_tokens][Hk][D] fp32 outputs.
+ */
+int oscar_step_write(const void* query_bf16, int64_t query_token_stride, const void* key_bf16,
+                     const void* value_bf16, int64_t kv_token_stride, int32_t num_tokens,
+                     int32_t num_heads, int32_t num_kv_heads, int32_t head_size, const float* rot_k,
+                     const float* rot_v, const int64_t* slot_mapping, const int32_t* query_start_loc,
+                     const int32_t* seq_lens, int32_t num_requests, void* k_cache, void* v_cache,
+                     int32_t block_size, int64_t num_pages, int64_t k_stride_page,
+                     int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
+                     int64_t v_stride_token, int64_t v_stride_head, int32_t clip_index_k,
+                     int32_t clip_index_v, float* stage_k, float* stage_v, int64_t* stage_owner,
+                     void* stage_k_image, void* stage_v_image, int32_t stage_rows, int32_t sink_eff,
+                     int32_t recent, float* q_rot, float* k_rot, float* v_rot, oscar_stream_t stream);
 
 /* ---------------------------------------------------------------- window write
  * Record the step's tokens in the FP32 sink/recent staging arena.

@@ -28,7 +28,7 @@ import torch
 
 from .config import OscarConfig
 from .format import HEAD_DIM, K_IDX_OFF, VALUES_PER_BYTE, check_d
-from .kernels import _lib, decode, prefill, quant, staging
+from .kernels import _lib, decode, prefill, quant, staging, step
 from .rotation import get_layer_rotation
 
 
@@ -250,6 +250,9 @@ class OscarAttentionBackendImpl:
             output[:num_tokens] = attn_out.reshape(output[:num_tokens].shape).to(output.dtype)
             return output
 
+        if self._short_step(layer, query, key, value, kv_cache, attn_metadata, output):
+            self._oscar_stats["reads"] += 1
+            return output
         self.do_kv_cache_update(layer, key, value, kv_cache,
                                 attn_metadata.slot_mapping[:attn_metadata.num_actual_tokens])
         if self._oscar.window_enabled:
@@ -263,6 +266,48 @@ class OscarAttentionBackendImpl:
         else:
             output[:num_tokens] = attn_out.reshape(num_tokens, -1).to(output.dtype)
         return output
+
+    def _short_step(self, layer, query, key, value, kv_cache, attn_metadata, output) -> bool:
+        """The whole forward of a step whose requests all take the paged read
+        (0 < q_len <= 16, backend.py:273-303) in two library calls: the fused
+        step write (q/k/v rotation, INT2 write, window write) and the decode
+        with R_v^T and the cast to the output dtype in its merge.  Returns
+        False (nothing done) when the step does not qualify."""
+        cfg = self._oscar
+        N = attn_metadata.num_actual_tokens
+        if not cfg.use_paged or N <= 0 or N > step.MAX_STEP_TOKENS or query.shape[0] < N:
+            return False
+        if output.dtype not in (torch.bfloat16, torch.float32) or query.dtype != torch.bfloat16 \
+                or key.dtype != torch.bfloat16 or value.dtype != torch.bfloat16:
+            return False
+        qsl, seqs = metadata_batch_lists(attn_metadata)
+        if qsl[0] != 0 or qsl[-1] != N or any(b - a < 0 or b - a > cfg.paged_max_q_len
+                                              for a, b in itertools.pairwise(qsl)):
+            return False
+        bs = self.key_cache.shape[1]
+        if bs % 32:
+            return False
+        dev = query.device
+        rk, rv = self._layer_rots(layer, dev)
+        stage = None
+        sink_eff = 0
+        if cfg.window_enabled:
+            self._ensure_staging(layer, kv_cache)
+            stage = (layer._oscar_stage_k, layer._oscar_stage_v, layer._oscar_slot_owner,
+                     layer._oscar_stage_kimg, layer._oscar_stage_vimg)
+            sink_eff = (cfg.sink_tokens // bs) * bs
+        D, Hq, Hk = self.head_size, self.num_heads, self.num_kv_heads
+        q_rot, k_rot, v_rot = step.step_write(
+            query, key, value, rk, rv, attn_metadata.slot_mapping[:N], qsl, seqs, self.key_cache,
+            self.value_cache, quant.clip_index(cfg.k_clip_ratio, D), quant.clip_index(cfg.v_clip_ratio, D),
+            Hq, Hk, stage, sink_eff, cfg.recent_tokens)
+        self._oscar_stats["writes"] += 1
+        self._oscar_stats["kv_bytes_written"] += N * Hk * 160
+        decode.paged_attention(q_rot, k_rot, v_rot, self.key_cache, self.value_cache, attn_metadata.block_tables,
+                               qsl, seqs, self.scale, stage, out_rotation=layer._oscar_rvT, out=output[:N])
+        if output.shape[0] > N:
+            output[N:].zero_()
+        return True
 
     def _decode_attention(self, layer, query, attn_metadata) -> torch.Tensor:
         """backend.py:321-358, 500-586 — one query token per request over its

@@ -30,6 +30,7 @@ COMMON = [
 ]
 PER_FILE = {
     "quant_write.hip": ["-ffp-contract=off"],
+    "step_write.hip": ["-ffp-contract=off"],
 }
 
 

@@ -970,6 +970,124 @@ __global__ __launch_bounds__(256) void paged_decode_merge_small_kernel(DecodeArg
   *reinterpret_cast<floatx4*>(a.out + ((int64_t)(it.qa + j) * a.num_heads + h) * kHeadDim + f0) = acc * inv;
 }
 
+// Merge with the output rotation (the reference's `out @ R_v^T`,
+// backend.py:293-295) and the cast to the model dtype fused in: one
+// 256-thread block per (output row, quarter of the output features) of an
+// item.  The block LSE-combines the row's partials over all 256 rotated
+// features (thread: partial group t / 64, features 4 (t % 64) .. +3), then
+// multiplies the normalised row by its quarter of R_v^T (wave w: rotated
+// features 64w .. 64w + 63 in order, lane: one output feature; the four
+// waves' sums are added in wave order) and writes it as fp32 or bf16 (RNE).
+__global__ __launch_bounds__(256) void paged_decode_merge_rotate_kernel(DecodeArgs a, const float* __restrict__ rot_t,
+                                                                        void* __restrict__ out, int64_t out_stride,
+                                                                        int out_bf16) {
+  __shared__ float wpart[kMaxPartials];
+  __shared__ float red[2][4];
+  __shared__ floatx4 osum[4][64];
+  __shared__ __attribute__((aligned(16))) float orow[kHeadDim];
+  __shared__ float csum[4][64];
+  const int qd = blockIdx.x & 3;
+  const int r = blockIdx.x >> 2;
+  const int item = blockIdx.y;
+  const int rt = blockIdx.z;
+  const ItemInfo it = a.items[item];
+  const int rows = it.nq * a.group;
+  const int row = rt * kRows + r;
+  if (it.nq <= 0 || row >= rows) return;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int steps = (it.prefix + kStepTok - 1) / kStepTok;
+  const int hs = min(a.max_splits, steps);
+  const int P = hs + a.fresh;
+  const float* base = a.ws + item_index(a, item, 0, rt) * kPartialFloats;
+  const int64_t pstride = (int64_t)a.row_tiles * kPartialFloats;
+  auto partial = [&](int p) { return base + (p < hs ? p : a.max_splits) * pstride; };
+
+  // ---- partial weights ----
+  float mreg[kMaxPartials / 256], lreg[kMaxPartials / 256];
+  float mloc = -__builtin_inff();
+#pragma unroll
+  for (int k = 0; k < kMaxPartials / 256; ++k) {
+    const int p = tid + 256 * k;
+    mreg[k] = -__builtin_inff();
+    lreg[k] = 0.f;
+    if (p < P) {
+      mreg[k] = partial(p)[kPartO + r];
+      lreg[k] = partial(p)[kPartO + kRows + r];
+    }
+    mloc = fmaxf(mloc, mreg[k]);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, o, 64));
+  if (lane == 0) red[0][w] = mloc;
+  __syncthreads();
+  const float mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  float lsum = 0.f;
+#pragma unroll
+  for (int k = 0; k < kMaxPartials / 256; ++k) {
+    const int p = tid + 256 * k;
+    if (p < P) {
+      const float wgt = (mreg[k] == -__builtin_inff()) ? 0.f : exp2f(mreg[k] - mx);
+      wpart[p] = wgt;
+      lsum = fmaf(wgt, lreg[k], lsum);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) lsum += __shfl_xor(lsum, o, 64);
+  if (lane == 0) red[1][w] = lsum;
+  __syncthreads();
+  const float L = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+
+  // ---- the row in the rotated domain ----
+  floatx4 acc = floatx4{};
+  constexpr int kBatch = 8;
+  for (int p0 = w; p0 < P; p0 += 4 * kBatch) {
+    floatx4 x[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int p = p0 + 4 * k;
+      x[k] = p < P ? *reinterpret_cast<const floatx4*>(partial(p) + r * kHeadDim + 4 * lane) : floatx4{};
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int p = p0 + 4 * k;
+      if (p < P) acc += wpart[p] * x[k];
+    }
+  }
+  osum[w][lane] = acc;
+  __syncthreads();
+  if (w == 0) {
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const floatx4 o = ((osum[0][lane] + osum[1][lane]) + osum[2][lane]) + osum[3][lane];
+    *reinterpret_cast<floatx4*>(&orow[4 * lane]) = o * inv;
+  }
+  __syncthreads();
+
+  // ---- out[64 qd + lane] = sum_f orow[f] * R_v^T[f][64 qd + lane] ----
+  const float* rt_col = rot_t + (int64_t)(64 * w) * kHeadDim + 64 * qd + lane;
+  float y = 0.f;
+#pragma unroll
+  for (int f0 = 0; f0 < 64; f0 += 16) {
+    float rv[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) rv[k] = rt_col[(int64_t)(f0 + k) * kHeadDim];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) y = fmaf(orow[64 * w + f0 + k], rv[k], y);
+  }
+  csum[w][lane] = y;
+  __syncthreads();
+  if (w == 0) {
+    const float o = ((csum[0][lane] + csum[1][lane]) + csum[2][lane]) + csum[3][lane];
+    const int j = row / a.group;
+    const int h = it.kvh * a.group + (row - j * a.group);
+    const int64_t idx = (int64_t)(it.qa + j) * out_stride + (int64_t)h * kHeadDim + 64 * qd + lane;
+    if (out_bf16)
+      reinterpret_cast<__bf16*>(out)[idx] = (__bf16)o;
+    else
+      reinterpret_cast<float*>(out)[idx] = o;
+  }
+}
+
 // DecodeOnly window bounds of the launch chunk's requests (backend.py:514-551):
 // win[2r] = head (sink_eff when the request is longer than the sink and every
 // seat of its sink pages holds that page, else 0), win[2r + 1] = cut (start of
@@ -1135,9 +1253,21 @@ int merge_rows(int64_t rows) { return (int)(rows < kRows ? rows : kRows); }
 
 // The merge of one launch chunk: the per-thread combine when every item has
 // at most kSmallP partials, else one block per (row, feature quarter).
-int launch_merge(const DecodeArgs& a, int64_t max_rows, unsigned nitems, hipStream_t stream) {
+struct OutRotation {
+  const float* rot_t;     // R_v^T [D][D], or null: rotated-V-domain fp32 output in a.out
+  void* out;              // [tokens][out_stride] fp32 or bf16
+  int64_t out_stride;     // elements per token
+  int32_t out_bf16;
+};
+
+int launch_merge(const DecodeArgs& a, int64_t max_rows, unsigned nitems, const OutRotation& orot,
+                 hipStream_t stream) {
   const int mr = merge_rows(max_rows);
-  if (a.max_splits + a.fresh <= kSmallP) {
+  if (orot.rot_t != nullptr) {
+    dim3 grid((unsigned)(mr * 4), nitems, (unsigned)a.row_tiles);
+    hipLaunchKernelGGL(paged_decode_merge_rotate_kernel, grid, dim3(256), 0, stream, a, orot.rot_t, orot.out,
+                       orot.out_stride, (int)orot.out_bf16);
+  } else if (a.max_splits + a.fresh <= kSmallP) {
     dim3 grid((unsigned)((mr * 4 + 15) / 16), nitems, (unsigned)a.row_tiles);
     hipLaunchKernelGGL(paged_decode_merge_small_kernel, grid, dim3(256), 0, stream, a);
   } else {
@@ -1169,19 +1299,21 @@ size_t oscar_paged_decode_workspace_bytes(int32_t num_requests, int32_t num_kv_h
   return workspace_floats(num_requests, num_kv_heads, num_heads, max_query_len, max_history, tps) * sizeof(float);
 }
 
-int oscar_paged_decode(const float* q_rot, const float* k_new, const float* v_new,
-                       int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
-                       int32_t head_size, const void* k_cache, const void* v_cache,
-                       int32_t block_size, int64_t num_pages, int64_t k_stride_page,
-                       int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
-                       int64_t v_stride_token, int64_t v_stride_head, const int32_t* block_table,
-                       int64_t block_table_stride, int32_t block_table_cols,
-                       const int32_t* query_start_loc, const int32_t* seq_lens,
-                       int32_t num_requests, int32_t max_query_len, int64_t max_history,
-                       const int64_t* stage_owner, const void* stage_k_image,
-                       const void* stage_v_image, int32_t stage_rows, float scale,
-                       int32_t tiles_per_split, float* out, void* workspace,
-                       size_t workspace_size, hipStream_t stream) {
+}  // extern "C"
+
+namespace oscar {
+namespace {
+
+int paged_decode(const float* q_rot, const float* k_new, const float* v_new, int32_t num_tokens, int32_t num_heads,
+                 int32_t num_kv_heads, int32_t head_size, const void* k_cache, const void* v_cache,
+                 int32_t block_size, int64_t num_pages, int64_t k_stride_page, int64_t k_stride_token,
+                 int64_t k_stride_head, int64_t v_stride_page, int64_t v_stride_token, int64_t v_stride_head,
+                 const int32_t* block_table, int64_t block_table_stride, int32_t block_table_cols,
+                 const int32_t* query_start_loc, const int32_t* seq_lens, int32_t num_requests,
+                 int32_t max_query_len, int64_t max_history, const int64_t* stage_owner,
+                 const void* stage_k_image, const void* stage_v_image, int32_t stage_rows, float scale,
+                 int32_t tiles_per_split, float* out, const OutRotation& orot, void* workspace,
+                 size_t workspace_size, hipStream_t stream) {
   if (head_size != kHeadDim) return kErrUnsupportedHeadDim;
   if (num_tokens < 0 || num_requests < 0 || num_heads <= 0 || num_kv_heads <= 0 ||
       num_kv_heads > kMaxInlineItems || num_heads % num_kv_heads != 0 || max_query_len < 0 ||
@@ -1234,9 +1366,63 @@ int oscar_paged_decode(const float* q_rot, const float* k_new, const float* v_ne
     dim3 grid((unsigned)(a.max_splits + 1), nitems, (unsigned)a.row_tiles);
     hipLaunchKernelGGL(paged_decode_split_kernel, grid, dim3(256), kLdsBytes, stream, a);
     if (hipGetLastError() != hipSuccess) return kErrLaunch;
-    if ((rc = launch_merge(a, (int64_t)max_query_len * a.group, nitems, stream)) != kOk) return rc;
+    if ((rc = launch_merge(a, (int64_t)max_query_len * a.group, nitems, orot, stream)) != kOk) return rc;
   }
   return kOk;
+}
+
+}  // namespace
+}  // namespace oscar
+
+extern "C" {
+
+int oscar_paged_decode(const float* q_rot, const float* k_new, const float* v_new,
+                       int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                       int32_t head_size, const void* k_cache, const void* v_cache,
+                       int32_t block_size, int64_t num_pages, int64_t k_stride_page,
+                       int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
+                       int64_t v_stride_token, int64_t v_stride_head, const int32_t* block_table,
+                       int64_t block_table_stride, int32_t block_table_cols,
+                       const int32_t* query_start_loc, const int32_t* seq_lens,
+                       int32_t num_requests, int32_t max_query_len, int64_t max_history,
+                       const int64_t* stage_owner, const void* stage_k_image,
+                       const void* stage_v_image, int32_t stage_rows, float scale,
+                       int32_t tiles_per_split, float* out, void* workspace,
+                       size_t workspace_size, hipStream_t stream) {
+  if (!out) return kErrInvalidArgument;
+  return paged_decode(q_rot, k_new, v_new, num_tokens, num_heads, num_kv_heads, head_size, k_cache, v_cache,
+                      block_size, num_pages, k_stride_page, k_stride_token, k_stride_head, v_stride_page,
+                      v_stride_token, v_stride_head, block_table, block_table_stride, block_table_cols,
+                      query_start_loc, seq_lens, num_requests, max_query_len, max_history, stage_owner,
+                      stage_k_image, stage_v_image, stage_rows, scale, tiles_per_split, out,
+                      OutRotation{nullptr, nullptr, 0, 0}, workspace, workspace_size, stream);
+}
+
+int oscar_paged_decode_rotated(const float* q_rot, const float* k_new, const float* v_new,
+                               int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                               int32_t head_size, const void* k_cache, const void* v_cache,
+                               int32_t block_size, int64_t num_pages, int64_t k_stride_page,
+                               int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
+                               int64_t v_stride_token, int64_t v_stride_head, const int32_t* block_table,
+                               int64_t block_table_stride, int32_t block_table_cols,
+                               const int32_t* query_start_loc, const int32_t* seq_lens,
+                               int32_t num_requests, int32_t max_query_len, int64_t max_history,
+                               const int64_t* stage_owner, const void* stage_k_image,
+                               const void* stage_v_image, int32_t stage_rows, float scale,
+                               int32_t tiles_per_split, const float* rot_v_t, void* out,
+                               int64_t out_token_stride, int32_t out_bf16, void* workspace,
+                               size_t workspace_size, hipStream_t stream) {
+  if (!rot_v_t || !out || out_token_stride < (int64_t)num_heads * kHeadDim || out_bf16 < 0 || out_bf16 > 1)
+    return kErrInvalidArgument;
+  // The merge blocks write their outputs through this pointer only; the
+  // fp32 rotated-domain output pointer of the split kernels is unused.
+  return paged_decode(q_rot, k_new, v_new, num_tokens, num_heads, num_kv_heads, head_size, k_cache, v_cache,
+                      block_size, num_pages, k_stride_page, k_stride_token, k_stride_head, v_stride_page,
+                      v_stride_token, v_stride_head, block_table, block_table_stride, block_table_cols,
+                      query_start_loc, seq_lens, num_requests, max_query_len, max_history, stage_owner,
+                      stage_k_image, stage_v_image, stage_rows, scale, tiles_per_split,
+                      reinterpret_cast<float*>(out), OutRotation{rot_v_t, out, out_token_stride, out_bf16},
+                      workspace, workspace_size, stream);
 }
 
 size_t oscar_decode_only_workspace_bytes(int32_t num_requests, int32_t num_kv_heads, int32_t num_heads,
@@ -1312,7 +1498,7 @@ int oscar_decode_only(const float* q_rot, int32_t num_heads, int32_t num_kv_head
       hipLaunchKernelGGL(paged_decode_split_kernel, grid, dim3(256), kLdsBytes, stream, a);
       if (hipGetLastError() != hipSuccess) return kErrLaunch;
     }
-    if ((rc = launch_merge(a, a.group, nitems, stream)) != kOk) return rc;
+    if ((rc = launch_merge(a, a.group, nitems, OutRotation{nullptr, nullptr, 0, 0}, stream)) != kOk) return rc;
   }
   return kOk;
 }

@@ -12,17 +12,8 @@
 // persistent int32 array that starts (and is left) at -1.  Kernel 2: one block
 // per token; the winner updates owner / values and resets its seat to -1.
 //
-// A kept winner also refreshes the fp16 operand images the decode kernel
-// reads for window-owned tokens, per (arena row, 32-token tile, kv head):
-//   K image [16 k-steps m][64 lanes][8 slots]: lane t + 32g, slot 2i + b of
-//     step m = 2j + a holds feature 128g + 16j + 4a + i + 8b of token t;
-//   V image [4 q][2 b][2 s][64 lanes][8 slots]: lane m + 32gs holds feature
-//     64q + 4(m >> 1) + 2b + (m & 1); slot u holds token 16s + 8gs +
-//     {0, 2, 1, 3, 4, 6, 5, 7}[u].
-// Both are exactly MFMA operand registers of the decode's wavefronts (K: the
-// tile's owner, V: wavefront q's quarter of the features), which read them
-// with one 16-byte load per lane and block.
-#include "oscar_common.h"
+// A kept winner also refreshes the fp16 operand images of window_images.h.
+#include "window_images.h"
 
 namespace oscar {
 namespace {
@@ -49,22 +40,6 @@ struct StageArgs {
   _Float16* kimg;           // [rows][bs / 32][Hk][8192] or null
   _Float16* vimg;
 };
-
-constexpr int kImgHalfs = 16 * 64 * 8;
-
-// Offsets of feature f of token t (0..31 within its tile) in the two images.
-__device__ __forceinline__ int kimg_offset(int f, int t) {
-  const int g = f >> 7, rr = f & 127, jj = rr >> 4, r16 = rr & 15, b = r16 >> 3, r8 = r16 & 7;
-  const int m = 2 * jj + (r8 >> 2), u = 2 * (r8 & 3) + b;
-  return (m * 64 + t + 32 * g) * 8 + u;
-}
-
-__device__ __forceinline__ int vimg_offset(int f, int t) {
-  const int q = f >> 6, b = (f >> 1) & 1, m = 2 * ((f >> 2) & 15) + (f & 1);
-  const int s = t >> 4, gs = (t >> 3) & 1, r = t & 7;
-  const int slot = r == 1 ? 2 : (r == 2 ? 1 : (r == 5 ? 6 : (r == 6 ? 5 : r)));   // self-inverse
-  return ((((q * 2 + b) * 2 + s) * 64) + m + 32 * gs) * 8 + slot;
-}
 
 __device__ __forceinline__ int64_t seat_of(int64_t slot, const StageArgs& a) {
   const int64_t page = slot / a.block_size;

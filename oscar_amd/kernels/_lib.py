@@ -35,6 +35,15 @@ SIGNATURES = {
                                     _c_p, _c_i64, _c_i32, _c_p, _c_p, _c_i32, _c_i32, _c_i64,
                                     _c_p, _c_p, _c_p, _c_i32, _c_f32, _c_i32, _c_p, _c_p, _c_sz,
                                     _c_p]),
+    "oscar_paged_decode_rotated": (_c_i32, [_c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_p,
+                                            _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                            _c_p, _c_i64, _c_i32, _c_p, _c_p, _c_i32, _c_i32, _c_i64,
+                                            _c_p, _c_p, _c_p, _c_i32, _c_f32, _c_i32, _c_p, _c_p, _c_i64,
+                                            _c_i32, _c_p, _c_sz, _c_p]),
+    "oscar_step_write": (_c_i32, [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_p,
+                                  _c_p, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_p, _c_i32, _c_i64, _c_i64, _c_i64,
+                                  _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p,
+                                  _c_p, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p]),
     "oscar_decode_only_workspace_bytes": (_c_sz, [_c_i32, _c_i32, _c_i32, _c_i64, _c_i32]),
     "oscar_decode_only": (_c_i32, [_c_p, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_i32, _c_i64, _c_i64,
                                    _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i32,

@@ -23,17 +23,11 @@ from .quant import cache_geometry
 
 MAX_QUERY_LEN = 16          # rows per request <= 16 tokens x group (backend.py:277)
 
-_workspaces: dict = {}
-
-
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per-device scratch for split partials, grown on demand (stream-ordered reuse)."""
-    key = (device.type, device.index)
-    ws = _workspaces.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _workspaces[key] = ws
-    return ws
+    """Scratch for one launch's split partials, from torch's caching allocator:
+    a block freed after a launch is reused by later launches on the same
+    stream only, so launches on different streams never share partials."""
+    return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
 
 
 def validate_layout(qsl, seqs):
@@ -82,7 +76,11 @@ def _stage_operands(stage, bs: int, hk: int):
 
 
 def plan(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None, out=None,
-         tiles_per_split: int = 0) -> DecodePlan:
+         tiles_per_split: int = 0, out_rotation=None) -> DecodePlan:
+    """One decode launch pair.  Without ``out_rotation`` the output is fp32
+    [n, Hq, D] in the rotated-V domain.  With ``out_rotation`` = R_v^T (fp32
+    [D, D]) the merge applies it and writes ``out`` (required: [n, Hq * D] or
+    [n, Hq, D], fp32 or bf16, unit feature stride) in the model domain."""
     n, hq, d = q.shape
     check_d(d)
     hk = k.shape[1]
@@ -115,20 +113,35 @@ def plan(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None, out=None,
         raise ValueError("paged decode needs a cache block size that is a multiple of 32")
     need = _lib.load().oscar_paged_decode_workspace_bytes(B, hk, hq, max(max_q, 1), max_hist, tiles_per_split)
     ws = workspace(dev, need)
-    if out is None:
-        out = torch.empty(n, hq, d, dtype=torch.float32, device=dev)
-    args = (_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), n, hq, hk, d, _lib.ptr(kc), _lib.ptr(vc), bs,
-            pages, *kst, *vst, _lib.ptr(bt), bt.stride(0), bt.shape[1], ctypes.addressof(qstart),
-            ctypes.addressof(seq_t), B, max_q, max_hist, _lib.ptr(owner), _lib.ptr(kimg), _lib.ptr(vimg), rows,
-            float(scale), int(tiles_per_split), _lib.ptr(out), _lib.ptr(ws), ws.numel())
-    return DecodePlan(args, out, [q, k, v, kc, vc, bt, qstart, seq_t, owner, kimg, vimg, ws])
+    common = (_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), n, hq, hk, d, _lib.ptr(kc), _lib.ptr(vc), bs,
+              pages, *kst, *vst, _lib.ptr(bt), bt.stride(0), bt.shape[1], ctypes.addressof(qstart),
+              ctypes.addressof(seq_t), B, max_q, max_hist, _lib.ptr(owner), _lib.ptr(kimg), _lib.ptr(vimg), rows,
+              float(scale), int(tiles_per_split))
+    keep = [q, k, v, kc, vc, bt, qstart, seq_t, owner, kimg, vimg, ws]
+    if out_rotation is None:
+        if out is None:
+            out = torch.empty(n, hq, d, dtype=torch.float32, device=dev)
+        return DecodePlan(common + (_lib.ptr(out), _lib.ptr(ws), ws.numel()), out, keep)
+    rot = out_rotation
+    if rot.shape != (d, d) or rot.dtype != torch.float32 or not rot.is_contiguous() or rot.device != dev:
+        raise ValueError("out_rotation must be a contiguous fp32 [D, D] tensor on the query's device")
+    if out is None or out.shape[0] < n or out.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("out_rotation needs an fp32 or bf16 output with a row per query token")
+    rows_out = out.reshape(out.shape[0], -1)
+    if rows_out.shape[1] != hq * d or rows_out.stride(1) != 1 or rows_out.data_ptr() != out.data_ptr():
+        raise ValueError("output rows must hold Hq * D contiguous features")
+    args = common + (_lib.ptr(rot), _lib.ptr(out), rows_out.stride(0), int(out.dtype == torch.bfloat16),
+                     _lib.ptr(ws), ws.numel())
+    return DecodePlan(args, out, keep + [rot], entry="oscar_paged_decode_rotated")
 
 
-def paged_attention(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None) -> torch.Tensor:
-    """Rotated-domain paged MTP attention; returns fp32 [n, Hq, D]."""
+def paged_attention(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None, out_rotation=None,
+                    out=None) -> torch.Tensor:
+    """Rotated-domain paged MTP attention; returns fp32 [n, Hq, D], or with
+    ``out_rotation`` (R_v^T) writes ``out`` in the model domain and returns it."""
     if q.shape[0] == 0:
-        return torch.empty(q.shape, dtype=torch.float32, device=q.device)
-    return plan(q, k, v, kc, vc, bt, qsl, seqs, scale, stage).launch()
+        return out if out is not None else torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    return plan(q, k, v, kc, vc, bt, qsl, seqs, scale, stage, out=out, out_rotation=out_rotation).launch()
 
 
 def decode_only_plan(q, kc, vc, bt, seqs, scale: float, stage=None, sink_tokens: int = 0,

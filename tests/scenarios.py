@@ -42,11 +42,25 @@ def metadata(slots, qsl, seqs, bt):
               block_tables=bt)
 
 
-def decode_case(history, q_lens, *, hq=6, hk=1, bs=128, pool_pages=None, seed=0,
-                clip=(0.96, 0.92), sink=128, recent=256, staging=8192, window=True,
-                cache_dtype=torch.int8, identity_pages=False, fill_bytes=False) -> DecodeCase:
+@dataclass
+class StepCase:
+    """A layer's state after its requests' history was written, and the
+    step that comes next (not yet written)."""
+    layer: OracleLayer
+    q: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+    qsl: list
+    seqs: list
+    bt: torch.Tensor
+    md: NS
+
+
+def step_case(history, q_lens, *, hq=6, hk=1, bs=128, pool_pages=None, seed=0,
+              clip=(0.96, 0.92), sink=128, recent=256, staging=8192, window=True,
+              cache_dtype=torch.int8, identity_pages=False, fill_bytes=False) -> StepCase:
     """Requests with the given history lengths write their history in one
-    prefill step, then write q_lens new tokens; returns the decode-step state.
+    prefill step; the returned case holds the next step's q_lens new tokens.
     fill_bytes: the caches start as random bytes (an engine's caches are not
     cleared), so slots nothing wrote hold arbitrary meta, NaN and inf included."""
     B = len(history)
@@ -82,7 +96,7 @@ def decode_case(history, q_lens, *, hq=6, hk=1, bs=128, pool_pages=None, seed=0,
     if sum(history):
         md = metadata(torch.cat(slots), qsl, list(history), bt)
         layer.write(torch.cat(hk_all), torch.cat(hv_all), md)
-    # Decode step: new tokens are written first (store + stage), then read.
+    # The next step's new tokens.
     n_tot = sum(q_lens)
     k, v = synthetic.kv(n_tot, hk, D, seed=seed * 1000 + 999)
     q = synthetic.queries(n_tot, hq, D, seed=seed * 1000 + 998)
@@ -92,5 +106,12 @@ def decode_case(history, q_lens, *, hq=6, hk=1, bs=128, pool_pages=None, seed=0,
         qsl.append(qsl[-1] + n)
     seqs = [h + n for h, n in zip(history, q_lens)]
     md = metadata(torch.cat(slots), qsl, seqs, bt)
-    layer.write(k, v, md)
-    return DecodeCase(layer, q, k, v, qsl, seqs, bt, md)
+    return StepCase(layer, q, k, v, qsl, seqs, bt, md)
+
+
+def decode_case(history, q_lens, **kw) -> DecodeCase:
+    """step_case, then the step's new tokens written (store + stage): the
+    state right before the step's read."""
+    c = step_case(history, q_lens, **kw)
+    c.layer.write(c.k, c.v, c.md)
+    return DecodeCase(c.layer, c.q, c.k, c.v, c.qsl, c.seqs, c.bt, c.md)

@@ -9,6 +9,7 @@ impl's output is bf16.  Stated tolerance: the bf16 contract's max-abs 2e-2
 plus half a bf16 ulp of the oracle value,
     |gpu - oracle| <= 2e-2 + 2^-8 * |oracle|   (elementwise).
 """
+import dataclasses
 from types import SimpleNamespace as NS
 
 import pytest
@@ -36,10 +37,8 @@ def make_impl(hq=6, hk=1, clip=(0.96, 0.92), sink=128, recent=256, staging=8192)
     impl.scale = D ** -0.5
     impl.key_cache = impl.value_cache = None
     impl._oscar_setup()
-    cfg = impl._oscar
-    cfg.k_clip_ratio, cfg.v_clip_ratio = clip
-    cfg.sink_tokens, cfg.recent_tokens, cfg.staging_tokens = sink, recent, staging
-    cfg.window_enabled = staging > 0 and (sink > 0 or recent > 0)
+    impl._oscar_cfg = dataclasses.replace(impl._oscar, k_clip_ratio=clip[0], v_clip_ratio=clip[1],
+                                          sink_tokens=sink, recent_tokens=recent, staging_tokens=staging)
     return impl
 
 

@@ -7,6 +7,7 @@ a DecodeOnly read without fresh K/V, each checked against the oracle layer
 fed the same inputs (reference plugin.py:73-181, integration.py:47-195,
 backend.py:239-319).  Tolerance: the bf16 contract |gpu - oracle| <= 2e-2 +
 2^-8 |oracle| elementwise (the oracle runs in fp32)."""
+import dataclasses
 import sys
 from types import ModuleType
 from types import SimpleNamespace as NS
@@ -75,8 +76,7 @@ def test_plugin_hooks_and_forward_routes(monkeypatch, capsys, device):
     plugin.load_plugin()
     attn = Attention("model.layers.1.self_attn.attn")
     assert isinstance(attn.impl, OscarAttentionBackendImpl) and engine.Worker._oscar_memory_hook
-    cfg = attn.impl._oscar
-    cfg.k_clip_ratio, cfg.v_clip_ratio = 0.96, 0.92
+    attn.impl._oscar_cfg = dataclasses.replace(attn.impl._oscar, k_clip_ratio=0.96, v_clip_ratio=0.92)
     engine.add_module(attn)
     worker = engine.Worker()
     budget = worker.determine_available_memory()
