@@ -1,38 +1,54 @@
 """Benchmark of the OSCAR INT2 KV-cache hot path on one MI355X.
 
-Headline metric: 4-token MTP decode attention over a 24,579-token
-INT2 history (Hq=6, Hk=1, D=256, 193 shuffled 128-token pages, FP32
-sink/recent window) in microseconds per layer and achieved HBM GB/s, plus the
+Headline metric: 4-token MTP decode attention over a 24,579-token INT2
+history (Hq=6, Hk=1, D=256, 193 shuffled 128-token pages, FP32 sink/recent
+window) in microseconds per layer and achieved HBM GB/s, plus the
 quantize-write GB/s of a 65,536-token bulk write (random slots, ~1/16
 skipped).
 
-A step is one layer's decode attention.  Steps cycle through `--layers`
-distinct per-layer caches (64 x ~13 MB, beyond the 256 MB Infinity Cache) so
-reads come from HBM.  The launches are captured once in a HIP graph and the
-graph is replayed; HIP events on the launch stream bracket exactly `--steps`
-layer decodes.  Inputs are resident in HBM before timing starts.
+A step is one layer's decode attention (`oscar_paged_decode`: split + merge
+kernels).  Steps cycle through `--layers` distinct per-layer caches (64 x ~13
+MB, beyond the 256 MB Infinity Cache) so reads come from HBM.  Exactly
+`--warmup` steps are replayed from one HIP graph, then exactly `--steps`
+steps from another, bracketed by device synchronisations and HIP events on
+the replay stream.  Inputs are resident in HBM before timing starts.
 
-cpu_baseline: the CPU oracle's read path (history dequant + window splice +
-causal SDPA, oracle/attention.py) on the same C2 inputs, timed on this host.
+Also in the line (config):
+* forward: the whole impl forward of the same MTP step per layer (fused step
+  write, decode, merge with R_v^T and the bf16 cast), timed the same way;
+* quant_write: the 65,536-token bulk write;
+* suite: the other workloads, each with its roofline, parity gate against
+  the oracle and the oracle's CPU time: 32 x 4 concurrent MTP decode, 8 x 1
+  long-context decode through the MTP and DecodeOnly entries, and the
+  15360 + 9256 prefill continuation.
+
+cpu_baseline: the CPU oracle's forward of the same step (rotate + clip +
+INT2 write + window write of the 4 new tokens, then history dequant + window
+splice + causal SDPA + output rotation, fp32) on this host's cores, and at 2
+threads as the reference's own harness runs.
 
 Prints one JSON line.
 """
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import statistics
 import sys
 import time
 from pathlib import Path
+from types import SimpleNamespace as NS
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 METRIC = "MTP decode attn µs/layer + HBM GB/s at 24K INT2 history; quant-write GB/s"
 HBM_PEAK_GBPS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
 C2_HISTORY, C2_QLEN, HQ, HK, D, BS = 24579, 4, 6, 1, 256, 128
+BF16_ABS, BF16_REL = 2e-2, 2.0 ** -8
 
 
 def log(msg):
@@ -41,57 +57,53 @@ def log(msg):
 
 class LayerState:
     """One FULL layer's state right before its decode read, written on the GPU
-    by the product write path (fused quantize-write + window-write kernels)."""
+    by the product write path, plus the step's own inputs."""
 
-    def __init__(self, impl, layer, caches, bt, qsl, seqs, q_rot, k_rot, v_rot):
+    def __init__(self, impl, layer, caches, bt, qsl, seqs, step):
         self.impl, self.layer, self.caches, self.bt = impl, layer, caches, bt
         self.qsl, self.seqs = qsl, seqs
-        self.q_rot, self.k_rot, self.v_rot = q_rot, k_rot, v_rot
+        self.step = step            # q, k, v (bf16), q_rot, k_rot, v_rot (fp32), md
 
     def stage(self):
         return self.impl._stage(self.layer)
 
 
-def make_impl(dev, window=True):
+def make_impl(window=True):
+    import contextlib
+    import io
+
     from oscar_amd.backend import OscarAttentionBackendImpl
 
     impl = OscarAttentionBackendImpl.__new__(OscarAttentionBackendImpl)
     impl.head_size, impl.num_kv_heads, impl.num_heads = D, HK, HQ
     impl.scale = D ** -0.5
     impl.key_cache = impl.value_cache = None
-    import contextlib
-    import io
-
     with contextlib.redirect_stdout(io.StringIO()):
         impl._oscar_setup()
-    cfg = impl._oscar
-    cfg.k_clip_ratio, cfg.v_clip_ratio = 0.96, 0.92
-    cfg.sink_tokens, cfg.recent_tokens, cfg.staging_tokens = 128, 256, 8192
-    cfg.window_enabled = window
+    impl._oscar_cfg = dataclasses.replace(impl._oscar, k_clip_ratio=0.96, v_clip_ratio=0.92, sink_tokens=128,
+                                          recent_tokens=256, staging_tokens=8192 if window else 0)
     return impl
 
 
 def build_layer(dev, history: list, q_len: int, pool: int, seed: int, window=True) -> LayerState:
-    """Prefill-write every request's history, then write the MTP step's tokens."""
-    from types import SimpleNamespace as NS
-
+    """Prefill-write every request's history, then write the step's tokens (bulk write path)."""
     import torch
 
     from oscar_amd import synthetic
 
-    impl = make_impl(dev, window)
+    impl = make_impl(window)
     Rk, Rv = synthetic.rotations(D, seed)
     layer = NS(layer_name="model.layers.0.self_attn.attn", _oscar_rots=(Rk.to(dev), Rv.to(dev)))
     caches = [torch.zeros(pool, BS, HK, D, dtype=torch.int8, device=dev) for _ in range(2)]
     B = len(history)
     need = [(h + q_len + BS - 1) // BS for h in history]
     perm = synthetic.page_permutation(pool, seed + 1)
-    T = max(need)
-    bt = torch.zeros(B, T, dtype=torch.int32)
+    bt = torch.zeros(B, max(need), dtype=torch.int32)
     off = 0
     for i, n in enumerate(need):
         bt[i, :n] = perm[off:off + n]
         off += n
+    btd = bt.to(dev)
 
     def write(counts, starts, seqs, kseed):
         n = sum(counts)
@@ -101,34 +113,31 @@ def build_layer(dev, history: list, q_len: int, pool: int, seed: int, window=Tru
         for c in counts:
             qsl.append(qsl[-1] + c)
         md = NS(num_actual_tokens=n, slot_mapping=slots.to(dev), query_start_loc_cpu=torch.tensor(qsl),
-                seq_lens_list=list(seqs), block_tables=bt.to(dev))
+                seq_lens_list=list(seqs), block_tables=btd)
         kd, vd = k.to(dev), v.to(dev)
         impl.do_kv_cache_update(layer, kd, vd, caches, md.slot_mapping)
         if window:
             impl._ensure_staging(layer, caches)
             impl._staging_write(layer, kd, vd, md)
-        return kd, vd, qsl
+        return kd, vd, md
 
     write(history, [0] * B, history, seed + 2)
     seqs = [h + q_len for h in history]
-    kd, vd, qsl = write([q_len] * B, history, seqs, seed + 3)
+    kd, vd, md = write([q_len] * B, history, seqs, seed + 3)
     q = synthetic.queries(q_len * B, HQ, D, seed=seed + 4).to(dev)
     rk, rv = layer._oscar_rots
     torch.cuda.synchronize()
-    return LayerState(impl, layer, caches, bt.to(dev), qsl, seqs, q.float() @ rk, kd.float() @ rk,
-                      vd.float() @ rv)
+    step = NS(q=q, k=kd, v=vd, q_rot=q.float() @ rk, k_rot=kd.float() @ rk, v_rot=vd.float() @ rv, md=md)
+    return LayerState(impl, layer, caches, btd, [int(x) for x in md.query_start_loc_cpu], seqs, step)
 
 
 def clone_layer(st: LayerState) -> LayerState:
-    from types import SimpleNamespace as NS
-
     layer = NS(**vars(st.layer))
     for name in ("_oscar_stage_k", "_oscar_stage_v", "_oscar_slot_owner", "_oscar_seat_winner",
                  "_oscar_stage_kimg", "_oscar_stage_vimg"):
         if getattr(st.layer, name, None) is not None:
             setattr(layer, name, getattr(st.layer, name).clone())
-    return LayerState(st.impl, layer, [c.clone() for c in st.caches], st.bt, st.qsl, st.seqs,
-                      st.q_rot, st.k_rot, st.v_rot)
+    return LayerState(st.impl, layer, [c.clone() for c in st.caches], st.bt, st.qsl, st.seqs, st.step)
 
 
 def decode_bytes(st: LayerState) -> dict:
@@ -140,7 +149,7 @@ def decode_bytes(st: LayerState) -> dict:
 
     owner = st.stage()[2].cpu() if st.stage() is not None else None
     bt = st.bt.cpu()
-    n_q = st.q_rot.shape[0]
+    n_q = st.step.q_rot.shape[0]
     hist_tokens = window = staged = 0
     for i, (a, b) in enumerate(zip(st.qsl, st.qsl[1:])):
         hist = st.seqs[i] - (b - a)
@@ -173,7 +182,7 @@ def decode_only_bytes(st: LayerState) -> dict:
     stage = st.stage()
     bt = st.bt.cpu()
     cfg = st.impl._oscar
-    n_q = st.q_rot.shape[0]
+    n_q = len(st.seqs)
     used = hist_tokens = owner_entries = 0
     for i, seq in enumerate(st.seqs):
         hist_tokens += seq
@@ -198,71 +207,95 @@ def decode_only_bytes(st: LayerState) -> dict:
             "int2_160B_variant": hist_tokens * HK * 160 + fixed}
 
 
-def bench_decode(args, dev, history, q_len, pool, layers, seed=93, decode_only=False):
+def graph_us(calls: list, steps: int, warmup: int) -> float:
+    """Mean µs per call of exactly `steps` calls (cycling through `calls`),
+    replayed from one HIP graph after `warmup` calls replayed from another."""
     import torch
 
-    from oscar_amd.kernels import decode
+    for c in calls:          # first-call setup (operands, arenas) stays out of the graphs
+        c()
+    torch.cuda.synchronize()
 
-    base = build_layer(dev, history, q_len, pool, seed, window=bool(args.window))
-    nbytes = decode_only_bytes(base) if decode_only else decode_bytes(base)
-    states = [base] + [clone_layer(base) for _ in range(layers - 1)]
-    if decode_only:
-        cfg = base.impl._oscar
-        plans = [decode.decode_only_plan(st.q_rot, st.caches[0], st.caches[1], st.bt, st.seqs, st.impl.scale,
-                                         st.stage(), cfg.sink_tokens, cfg.recent_tokens, tiles_per_split=args.tps)
-                 for st in states]
-    else:
-        plans = [decode.plan(st.q_rot, st.k_rot, st.v_rot, st.caches[0], st.caches[1], st.bt, st.qsl,
-                             st.seqs, st.impl.scale, st.stage(), tiles_per_split=args.tps) for st in states]
+    def capture(count):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(count):
+                calls[i % len(calls)]()
+        return g
+
+    warm = capture(warmup) if warmup > 0 else None
+    timed = capture(steps)
+    if warm is not None:
+        warm.replay()
     torch.cuda.synchronize()
-    side = torch.cuda.Stream(dev)
-    side.wait_stream(torch.cuda.current_stream(dev))
-    with torch.cuda.stream(side):
-        for p in plans:
-            p.launch()
-    torch.cuda.current_stream(dev).wait_stream(side)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for p in plans:
-            p.launch()
-    reps_w = max(1, args.warmup // layers)
-    reps = max(1, args.steps // layers)
-    for _ in range(reps_w):
-        graph.replay()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
+    stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
-    for _ in range(reps):
-        graph.replay()
+    timed.replay()
     e1.record(stream)
-    e1.synchronize()
-    steps = reps * layers
-    ms = e0.elapsed_time(e1)
-    us = ms * 1000.0 / steps
-    out0 = plans[0].launch().clone()
     torch.cuda.synchronize()
-    return {"us_per_layer": us, "steps": steps, "ms": ms, "gbps": nbytes["total"] / (us * 1e-6) / 1e9,
-            "bytes": nbytes, "state": base, "out0": out0, "warmup": reps_w * layers}
+    return e0.elapsed_time(e1) * 1000.0 / steps
 
 
-def bench_quant_write(args, dev):
+def layer_states(dev, history, q_len, pool, layers, seed=93, window=True):
+    base = build_layer(dev, history, q_len, pool, seed, window=window)
+    return [base] + [clone_layer(base) for _ in range(layers - 1)]
+
+
+def last_queries(st: LayerState):
+    """One rotated query per request: each request's last step token."""
+    return st.step.q_rot[[b - 1 for b in st.qsl[1:]]].contiguous()
+
+
+def bench_decode(dev, states, steps, warmup, tps=0, decode_only=False):
+    from oscar_amd.kernels import decode
+
+    base = states[0]
+    nbytes = decode_only_bytes(base) if decode_only else decode_bytes(base)
+    if decode_only:
+        cfg = base.impl._oscar
+        q1 = last_queries(base)
+        plans = [decode.decode_only_plan(q1, st.caches[0], st.caches[1], st.bt, st.seqs, st.impl.scale,
+                                         st.stage(), cfg.sink_tokens, cfg.recent_tokens, tiles_per_split=tps)
+                 for st in states]
+    else:
+        s = base.step
+        plans = [decode.plan(s.q_rot, s.k_rot, s.v_rot, st.caches[0], st.caches[1], st.bt, st.qsl, st.seqs,
+                             st.impl.scale, st.stage(), tiles_per_split=tps) for st in states]
+    us = graph_us([p.launch for p in plans], steps, warmup)
+    out0 = plans[0].launch().clone()
+    return {"us": us, "gbps": nbytes["total"] / (us * 1e-6) / 1e9, "bytes": nbytes, "out0": out0}
+
+
+def bench_forward(dev, states, steps, warmup):
+    """The impl forward of the MTP step on every layer state (fused step write,
+    decode, merge with R_v^T and the bf16 cast)."""
+    import torch
+
+    outs = [torch.empty(st.step.q.shape[0], HQ * D, dtype=torch.bfloat16, device=dev) for st in states]
+
+    def call(st, out):
+        s = st.step
+        return lambda: st.impl.forward(st.layer, s.q, s.k, s.v, st.caches, s.md, output=out)
+
+    us = graph_us([call(st, o) for st, o in zip(states, outs)], steps, warmup)
+    return {"us": us, "out0": outs[0].clone()}
+
+
+def bench_quant_write(dev, steps=64):
     import torch
 
     from oscar_amd import synthetic
-    from oscar_amd.kernels import _lib, quant
+    from oscar_amd.kernels import quant
 
     N = 65536
     pages = N // BS + 32
-    sets = 4
     g = torch.Generator().manual_seed(55)
     Rk, Rv = synthetic.rotations(D, seed=56)
     ops = [quant.rotation_operand(R.to(dev)) for R in (Rk, Rv)]
-    launches = []
-    keep = []
+    calls, keep = [], []
     valid_total = 0
-    for s in range(sets):
+    for s in range(4):
         k, v = synthetic.kv(N, HK, D, seed=100 + s)
         slots = torch.randperm(pages * BS, generator=g)[:N].to(torch.int64)
         slots[torch.rand(N, generator=g) < 1 / 16] = -1
@@ -271,26 +304,35 @@ def bench_quant_write(args, dev):
         kc = torch.zeros(pages, BS, HK, D, dtype=torch.int8, device=dev)
         vc = torch.zeros_like(kc)
         keep += [kd, vd, sd, kc, vc]
-        bs, npages, kst, vst = quant.cache_geometry(kc, vc)
-        launches.append((_lib.ptr(kd), _lib.ptr(vd), N, HK, D, HK * D, _lib.ptr(ops[0]), _lib.ptr(ops[1]),
-                         _lib.ptr(sd), _lib.ptr(kc), _lib.ptr(vc), bs, npages, *kst, *vst, 245, 235))
-    valid = valid_total / sets
+        calls.append(lambda kd=kd, vd=vd, sd=sd, kc=kc, vc=vc: quant.quant_write(
+            kd, vd, ops[0], ops[1], kc, vc, sd, 245, 235, HK, D))
+    valid = valid_total / 4
     nbytes = N * HK * 2 * D * 2 + valid * HK * 136 + N * 8 + 2 * D * D * 4
-    stream = torch.cuda.current_stream(dev)
-    h = stream.cuda_stream
-    for i in range(8):
-        _lib.call("oscar_quant_write", *launches[i % sets], h)
-    torch.cuda.synchronize()
-    iters = max(8, args.qw_iters)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for i in range(iters):
-        _lib.call("oscar_quant_write", *launches[i % sets], h)
-    e1.record(stream)
-    e1.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / iters
-    return {"us_per_call": us, "gbps": nbytes / (us * 1e-6) / 1e9, "bytes": nbytes, "tokens": N,
-            "valid_slots": valid}
+    us = graph_us(calls, steps, 8)
+    return {"us": us, "gbps": nbytes / (us * 1e-6) / 1e9, "bytes": nbytes, "steps": steps}
+
+
+def bench_prefill(dev, reps=10, seed=71):
+    """The prefill-continuation kernel on the written 15360 + 9256 state."""
+    from oscar_amd.kernels import prefill
+
+    hist, new = 15360, 9256
+    st = build_layer(dev, [hist], new, pool=(hist + new + BS - 1) // BS, seed=seed)
+    stage = st.stage()
+    stage3 = None if stage is None else stage[:3]
+    s = st.step
+    res = {}
+
+    def run():
+        res["out"] = prefill.prefill_continuation(s.q_rot, s.k_rot, s.v_rot, st.caches[0], st.caches[1],
+                                                  st.bt[0], hist, st.impl.scale, stage3)
+
+    us = graph_us([run], reps, 2)
+    run()
+    visible = new * (hist + 1) + new * (new - 1) // 2
+    flops = 4 * D * HQ * visible
+    return {"us": us, "flops": flops, "tflops": flops / (us * 1e-6) / 1e12, "state": st, "out0": res["out"],
+            "steps": reps}
 
 
 def copy_probe(dev, mib: int) -> None:
@@ -325,202 +367,211 @@ def traffic_from_profile(kernel_src: Path):
         return None
 
 
-def decode_only_cpu_baseline(st, gpu_out, seconds: float):
-    """The oracle's DecodeOnly read (INT2 middle + FP32 sink/tail, LSE merge) on
-    the same GPU-written state, on this host, and the parity of the timed kernel
-    against it (fp32 contract for this read: 2e-3 relative to the output scale)."""
-    import torch
-
-    from oracle import attention as oatt
-
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    q, kc, vc, bt = st.q_rot.cpu(), st.caches[0].cpu(), st.caches[1].cpu(), st.bt.cpu()
-    stage = st.stage()
-    cfg = st.impl._oscar
-    arena = None
-    if stage is not None:
-        arena = (stage[0].cpu(), stage[1].cpu(), stage[2].cpu(), (cfg.sink_tokens // BS) * BS, cfg.recent_tokens)
-
-    def once():
-        return oatt.decode_only_ref(q, kc, vc, bt, st.seqs, st.impl.scale, HK, D, arena)
-
-    want = once()
-    rel = (gpu_out.cpu() - want).abs().max().item() / max(want.abs().max().item(), 1e-30)
-    samples = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(samples) < 6:
-        t0 = time.perf_counter()
-        once()
-        samples.append(time.perf_counter() - t0)
-    return {"value": round(statistics.median(samples) * 1e6, 1), "unit": "us/layer", "cores": cores,
-            "kind": "port", "sample": f"median of {len(samples)} runs of the oracle DecodeOnly read on the same "
-                                      f"state ({sum(st.seqs)}-token INT2 history, FP32 sink + tail, fp32)"}, rel
-
-
-def cpu_baseline(st, gpu_out, seconds: float, label: str = "C2"):
-    """The oracle's read path on the same (GPU-written) C2 state, on this host.
-
-    Also the parity gate of the measured kernel: its output must match the
-    oracle within the fp32 contract (1e-3 relative to the output scale).
-    """
-    import torch
-
-    from oracle import attention as oatt
-
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    q, k, v = st.q_rot.cpu(), st.k_rot.cpu(), st.v_rot.cpu()
-    kc, vc = st.caches[0].cpu(), st.caches[1].cpu()
-    bt = st.bt.cpu()
-    stage = tuple(t.cpu() for t in st.stage()[:3]) if st.stage() is not None else None
-
-    def once():
-        return oatt.paged_attention_ref(q, k, v, kc, vc, bt, st.qsl, st.seqs, st.impl.scale, stage)
-
-    want = once()
-    rel = (gpu_out.cpu() - want).abs().max().item() / max(want.abs().max().item(), 1e-30)
-    samples = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(samples) < 6:
-        t0 = time.perf_counter()
-        once()
-        samples.append(time.perf_counter() - t0)
-    med = statistics.median(samples)
+# ---------------------------------------------------------------- CPU oracle
+def cpu_model() -> str:
     try:
-        model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+        return next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
     except Exception:
-        model = "unknown"
+        return "unknown"
+
+
+def timed_median(fn, seconds: float, min_runs: int = 6):
+    """One warm-up, then the median of at least min_runs runs or `seconds`."""
+    fn()
+    samples = []
+    t_end = time.perf_counter() + seconds
+    while len(samples) < min_runs or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        samples.append(time.perf_counter() - t0)
+    return statistics.median(samples), len(samples)
+
+
+def oracle_layer(st: LayerState):
+    """The oracle's layer over CPU copies of a GPU-written state."""
+    from oracle.forward import OracleLayer
+    from oracle.staging import Arena
+
+    cfg = st.impl._oscar
+    rk, rv = (r.cpu() for r in st.layer._oscar_rots)
+    L = OracleLayer(st.caches[0].cpu(), st.caches[1].cpu(), rk, rv, HQ, HK, D, st.impl.scale, cfg.k_clip_ratio,
+                    cfg.v_clip_ratio, cfg.sink_tokens, cfg.recent_tokens, cfg.staging_tokens)
+    stage = st.stage()
+    if stage is not None:
+        L.arena = Arena(stage[0].cpu(), stage[1].cpu(), stage[2].cpu(), BS, (cfg.sink_tokens // BS) * BS,
+                        cfg.recent_tokens)
+    return L
+
+
+def cpu_forward_baseline(st: LayerState, gpu_read, gpu_forward, seconds: float):
+    """The oracle's forward of the step (write of the new tokens + read + output
+    rotation) on this host, at all cores and at 2 threads, and the parity of the
+    GPU decode (fp32, 1e-3 of the output scale) and forward (bf16 contract)."""
+    import torch
+
+    from oracle import attention as oatt
+
+    L = oracle_layer(st)
+    s = st.step
+    md = NS(num_actual_tokens=s.md.num_actual_tokens, slot_mapping=s.md.slot_mapping.cpu(),
+            query_start_loc_cpu=s.md.query_start_loc_cpu, seq_lens_list=s.md.seq_lens_list,
+            block_tables=st.bt.cpu())
+    q, k, v = s.q.cpu(), s.k.cpu(), s.v.cpu()
+    # parity on the GPU-written state (the forward rewrote the step's tokens the same way)
+    want_read = oatt.paged_attention_ref(s.q_rot.cpu(), s.k_rot.cpu(), s.v_rot.cpu(), L.k_cache, L.v_cache,
+                                         md.block_tables, st.qsl, st.seqs, L.scale, L.stage())
+    read_rel = (gpu_read.cpu() - want_read).abs().max().item() / max(want_read.abs().max().item(), 1e-30)
+    fwd_ok, fwd_err = None, None
+    if gpu_forward is not None:
+        want_fwd = (want_read @ L.R_v.t()).reshape(gpu_forward.shape)
+        got = gpu_forward.cpu().float()
+        fwd_ok = bool(((got - want_fwd).abs() <= BF16_ABS + BF16_REL * want_fwd.abs()).all())
+        fwd_err = (got - want_fwd).abs().max().item()
+
+    def once():
+        L.forward(q.float(), k.float(), v.float(), md)
+
+    cores = len(os.sched_getaffinity(0))
+    res = {}
+    for threads in (cores, 2):
+        torch.set_num_threads(threads)
+        res[threads] = timed_median(once, seconds)
+    torch.set_num_threads(cores)
+    med, n = res[cores]
     base = {"value": round(med * 1e6, 1), "unit": "us/layer", "cores": cores, "kind": "port",
-            "sample": f"median of {len(samples)} runs (~{seconds:.0f} s) of the oracle read path on the {label} "
-                      f"layer state (dequant {sum(st.seqs) - q.shape[0]}-token INT2 history + FP32 window splice "
-                      f"+ causal SDPA, {q.shape[0]} queries x {q.shape[1]} heads, fp32); host CPU {model}"}
-    return base, rel
+            "value_2_threads": round(res[2][0] * 1e6, 1),
+            "sample": f"median of {n} runs (~{seconds:.0f} s) of the oracle forward of the C2 MTP step on the "
+                      f"GPU-written layer state: rotate + clip + INT2 write + window write of the 4 new tokens, "
+                      f"then dequant of the {sum(st.seqs) - q.shape[0]}-token INT2 history + window splice + "
+                      f"causal SDPA (4 queries x 6 heads) + output rotation, fp32; the same at 2 threads "
+                      f"({res[2][1]} runs) in value_2_threads; host CPU {cpu_model()}"}
+    return base, read_rel, fwd_ok, fwd_err
 
 
-SUITE = {
-    "C3": {"workload": "C3: concurrent MTP decode, 32 requests x 4 query tokens, Hq=6 Hk=1 D=256, histories "
-                       "uniform in [2048, 16384] in 128-token pages drawn from a shared 8192-page pool, FP32 "
-                       "sink=128/recent=256 window (staging 8192), clip 0.96/0.92, 16 distinct layers",
-           "q_len": 4, "pool": 8192, "layers": 16},
-    "C5-decode": {"workload": "C5 decode: 8 requests x 1 query token, 32768-token histories, Hq=6 Hk=1 D=256, "
-                              "pages scattered over a 2056-page pool (2048 history pages + 8 for the step's "
-                              "token), FP32 sink=128/recent=256 window (staging 8192), 16 distinct layers",
-                  "q_len": 1, "pool": 2056, "layers": 16},
-    "C2-decode-only": {"workload": "C2 DecodeOnly: the read without fresh K/V, 1 request x 1 query token over "
-                                   "its whole 24580-token INT2 history in 193 shuffled 128-token pages, Hq=6 "
-                                   "Hk=1 D=256, FP32 sink=128/recent=256 window (staging 8192), 64 distinct layers",
-                       "q_len": 1, "pool": 193, "layers": 64, "decode_only": True},
-    "C4": {"workload": "C4: prefill continuation, 1 request, 15360-token INT2 history + 9256 new tokens "
-                       "(causal over history + new), Hq=6 Hk=1 D=256, 128-token pages, FP32 window"},
-}
-MFMA_BF16_PEAK_TFLOPS = 2500.0
+def cpu_read_baseline(st: LayerState, gpu_out, seconds: float, decode_only=False):
+    """The oracle's read on the same state (the paged MTP read, or the
+    DecodeOnly windowed read) and the parity of the GPU output against it."""
+    import torch
+
+    from oracle import attention as oatt
+
+    L = oracle_layer(st)
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    bt = st.bt.cpu()
+    if decode_only:
+        q = last_queries(st).cpu()
+        A = L.arena
+        arena = None if A is None else (A.stage_k, A.stage_v, A.owner, A.sink_eff, L.recent)
+
+        def once():
+            return oatt.decode_only_ref(q, L.k_cache, L.v_cache, bt, st.seqs, L.scale, HK, D, arena)
+    else:
+        s = st.step
+        q, k, v = s.q_rot.cpu(), s.k_rot.cpu(), s.v_rot.cpu()
+
+        def once():
+            return oatt.paged_attention_ref(q, k, v, L.k_cache, L.v_cache, bt, st.qsl, st.seqs, L.scale, L.stage())
+
+    want = once()
+    rel = (gpu_out.cpu() - want).abs().max().item() / max(want.abs().max().item(), 1e-30)
+    med, n = timed_median(once, seconds, min_runs=3)
+    return {"value": round(med * 1e6, 1), "unit": "us/layer", "cores": cores, "kind": "port",
+            "sample": f"median of {n} runs of the oracle {'DecodeOnly' if decode_only else 'paged MTP'} read "
+                      f"on the same GPU-written state, fp32"}, rel
 
 
+def cpu_prefill_baseline(st: LayerState, gpu_out, seconds: float):
+    """The oracle's dense read for the continuation (dequant + splice + chunked
+    causal SDPA, fp32) and the parity of the kernel (bf16 contract)."""
+    import torch
+
+    from oracle import attention as oatt
+
+    L = oracle_layer(st)
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    s = st.step
+    q, k, v = s.q_rot.cpu(), s.k_rot.cpu(), s.v_rot.cpu()
+    bt = st.bt.cpu()
+    res = {}
+
+    def once():
+        res["want"] = oatt.paged_attention_ref(q, k, v, L.k_cache, L.v_cache, bt, st.qsl, st.seqs, L.scale,
+                                               L.stage())
+
+    med, n = timed_median(once, seconds, min_runs=2)
+    got, want = gpu_out.cpu(), res["want"]
+    ok = bool(((got - want).abs() <= BF16_ABS + BF16_REL * want.abs()).all())
+    return {"value": round(med * 1e3, 1), "unit": "ms/layer", "cores": cores, "kind": "port",
+            "sample": f"median of {n} runs of the oracle dense read of the 15360 + 9256 state, fp32"}, ok, \
+        (got - want).abs().max().item()
+
+
+# ---------------------------------------------------------------- suite
 def suite_histories(name: str):
     import torch
 
     if name == "C3":
         g = torch.Generator().manual_seed(2024)
         return [int(x) for x in torch.randint(2048, 16385, (32,), generator=g)]
-    if name == "C2-decode-only":
-        return [24579]
     return [32768] * 8
 
 
-def bench_prefill(args, dev, seed=71):
-    """C4: the prefill-continuation kernel on the written 15360 + 9256 state."""
-    import torch
-
-    from oscar_amd.kernels import prefill
-
-    hist, new = 15360, 9256
-    st = build_layer(dev, [hist], new, pool=(hist + new + BS - 1) // BS, seed=seed)
-    stage = st.stage()
-    stage3 = None if stage is None else stage[:3]
-
-    def run():
-        return prefill.prefill_continuation(st.q_rot, st.k_rot, st.v_rot, st.caches[0], st.caches[1],
-                                            st.bt[0], hist, st.impl.scale, stage3)
-
-    for _ in range(2):
-        out = run()
-    torch.cuda.synchronize()
-    reps = 10
-    stream = torch.cuda.current_stream(dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(reps):
-        run()
-    e1.record(stream)
-    e1.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / reps
-    visible = new * (hist + 1) + new * (new - 1) // 2
-    flops = 4 * D * HQ * visible
-    return {"us": us, "flops": flops, "tflops": flops / (us * 1e-6) / 1e12, "state": st, "out0": out}
+SUITE = {
+    "C3": {"workload": "32 requests x 4 MTP query tokens, Hq=6 Hk=1 D=256, histories uniform in [2048, 16384] "
+                       "in 128-token pages drawn from a shared 8192-page pool, FP32 sink=128/recent=256 window "
+                       "(staging 8192), clip 0.96/0.92, 16 distinct layers",
+           "q_len": 4, "pool": 8192, "layers": 16},
+    "C5_decode": {"workload": "8 requests x 1 query token, 32768-token histories, Hq=6 Hk=1 D=256, pages "
+                              "scattered over a 2056-page pool (2048 history pages + 8 for the step's token), "
+                              "FP32 sink=128/recent=256 window (staging 8192), 16 distinct layers",
+                  "q_len": 1, "pool": 2056, "layers": 16},
+    "C5_decode_only": {"workload": "the same 8 x 32768 state read through the DecodeOnly entry (no fresh K/V, "
+                                   "one query per request over its whole 32769-token history)",
+                       "q_len": 1, "pool": 2056, "layers": 16, "decode_only": True},
+    "C4": {"workload": "prefill continuation, 1 request, 15360-token INT2 history + 9256 new tokens (causal "
+                       "over history + new), Hq=6 Hk=1 D=256, 128-token pages, FP32 window"},
+}
 
 
-def prefill_cpu_baseline(st, gpu_out, hist: int, seconds: float):
-    """The oracle's dense read path for C4 (dequant + splice + chunked causal SDPA), and the parity
-    of the timed kernel against it (bf16 contract: 2e-2 + 2^-8 |oracle| elementwise)."""
-    import torch
-
-    from oracle import attention as oatt
-
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    q, k, v = st.q_rot.cpu(), st.k_rot.cpu(), st.v_rot.cpu()
-    kc, vc, bt = st.caches[0].cpu(), st.caches[1].cpu(), st.bt.cpu()
-    stage = tuple(t.cpu() for t in st.stage()[:3]) if st.stage() is not None else None
-    samples, want = [], None
-    t_end = time.perf_counter() + seconds
-    while not samples or (time.perf_counter() < t_end and len(samples) < 6):
-        t0 = time.perf_counter()
-        want = oatt.paged_attention_ref(q, k, v, kc, vc, bt, st.qsl, st.seqs, st.impl.scale, stage)
-        samples.append(time.perf_counter() - t0)
-    got = gpu_out.cpu()
-    ok = bool(((got - want).abs() <= 2e-2 + 2.0 ** -8 * want.abs()).all())
-    err = (got - want).abs().max().item()
-    return {"value": round(statistics.median(samples) * 1e3, 1), "unit": "ms/layer", "cores": cores,
-            "kind": "port", "sample": f"median of {len(samples)} runs of the oracle dense read path on the "
-                                      f"C4 state (dequant + window splice + chunked causal SDPA, fp32)"}, ok, err
-
-
-def suite(args, dev):
-    """One JSON line per extra workload: C3 and C5 decode (HBM roofline), C4 prefill (MFMA roofline)."""
-    for name in args.suite.split(","):
+def suite(dev, names, cpu_seconds, steps=64):
+    out = {}
+    long_states = None
+    for name in names:
         cfg = SUITE[name]
+        log(f"bench: suite {name}")
         if name == "C4":
-            r = bench_prefill(args, dev)
-            cpu, ok, err = prefill_cpu_baseline(r["state"], r["out0"], 15360, args.cpu_seconds)
+            r = bench_prefill(dev)
+            cpu, ok, err = cpu_prefill_baseline(r["state"], r["out0"], cpu_seconds)
             if not ok:
                 raise SystemExit(f"C4 parity gate failed: max abs err {err:.3e}")
-            line = {"config": name, "workload": cfg["workload"], "value": round(r["us"], 2),
-                    "unit": "us/layer", "arith": "bf16-contract: INT2 dequant to f16, f16 MFMA, f32 softmax",
-                    "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1),
-                                 "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                 "frac": round(r["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4), "flops": r["flops"]},
-                    "parity_max_abs_err": err, "cpu_baseline": cpu}
+            out[name] = {"workload": cfg["workload"], "value": round(r["us"], 2), "unit": "us/layer",
+                         "steps": r["steps"],
+                         "arith": "bf16 contract: INT2 codes as exact f16 operands, f16 MFMA, f32 softmax",
+                         "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1),
+                                      "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                      "frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4), "flops": r["flops"]},
+                         "parity_max_abs_err": err, "cpu_baseline": cpu}
+            continue
+        only = cfg.get("decode_only", False)
+        if name.startswith("C5") and long_states is not None:
+            states = long_states
         else:
-            hist = suite_histories(name)
-            only = cfg.get("decode_only", False)
-            dec = bench_decode(args, dev, hist, cfg["q_len"], pool=cfg["pool"], layers=cfg["layers"],
-                               decode_only=only)
-            if only:
-                cpu, rel = decode_only_cpu_baseline(dec["state"], dec["out0"], args.cpu_seconds)
-            else:
-                cpu, rel = cpu_baseline(dec["state"], dec["out0"], args.cpu_seconds, name)
-            if not rel <= (2e-3 if only else 1e-3):
-                raise SystemExit(f"{name} parity gate failed: rel err {rel:.3e}")
-            line = {"config": name, "workload": cfg["workload"], "value": round(dec["us_per_layer"], 3),
-                    "unit": "us/layer", "steps": dec["steps"],
-                    "roofline": {"bound": "hbm", "achieved": round(dec["gbps"], 1), "peak": HBM_PEAK_GBPS,
-                                 "unit": "GB/s", "frac": round(dec["gbps"] / HBM_PEAK_GBPS, 4),
-                                 "bytes_per_layer": dec["bytes"]["total"]},
-                    "history_tokens": sum(dec["state"].seqs) if only else sum(hist),
-                    "staged_tokens": dec["bytes"]["staged_tokens"],
-                    "parity_rel_err": rel, "cpu_baseline": cpu}
-        print(json.dumps(line), flush=True)
+            states = layer_states(dev, suite_histories(name), cfg["q_len"], cfg["pool"], cfg["layers"])
+            if name.startswith("C5"):
+                long_states = states
+        dec = bench_decode(dev, states, steps, 16, decode_only=only)
+        cpu, rel = cpu_read_baseline(states[0], dec["out0"], cpu_seconds, decode_only=only)
+        if not rel <= 1e-3:
+            raise SystemExit(f"{name} parity gate failed: rel err {rel:.3e}")
+        out[name] = {"workload": cfg["workload"], "value": round(dec["us"], 3), "unit": "us/layer",
+                     "steps": steps,
+                     "roofline": {"bound": "hbm", "achieved": round(dec["gbps"], 1), "peak": HBM_PEAK_GBPS,
+                                  "unit": "GB/s", "frac": round(dec["gbps"] / HBM_PEAK_GBPS, 4),
+                                  "bytes_per_layer": dec["bytes"]["total"]},
+                     "staged_tokens": dec["bytes"]["staged_tokens"], "parity_rel_err": rel, "cpu_baseline": cpu}
+    return out
 
 
 def main():
@@ -529,76 +580,92 @@ def main():
     ap.add_argument("--steps", type=int, default=640)
     ap.add_argument("--warmup", type=int, default=128)
     ap.add_argument("--layers", type=int, default=64)
-    ap.add_argument("--qw-iters", type=int, default=64)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--suite-cpu-seconds", type=float, default=4.0)
     ap.add_argument("--tps", type=int, default=0, help="decode tiles per split (0: automatic)")
-    ap.add_argument("--skip-quant-write", action="store_true")
     ap.add_argument("--window", type=int, default=1, help="diagnostic: 0 disables the FP32 window")
+    ap.add_argument("--parts", default="forward,quant_write,suite,cpu",
+                    help="comma list of what runs besides the headline decode "
+                         "(forward, quant_write, suite, cpu; empty: the decode only)")
+    ap.add_argument("--suite", default="C3,C5_decode,C5_decode_only,C4", help="suite workloads")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run a plain device copy of this many MiB first (PMC byte-counter calibration)")
-    ap.add_argument("--suite", default="",
-                    help="comma list of extra workloads (C3, C5-decode, C2-decode-only, C4): one JSON "
-                         "line each instead of the headline line")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (one TP rank's share "
-              "per GPU, no collectives); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (one TP rank's share per GPU, no "
+              "collectives); run with --gpus 1", file=sys.stderr)
         raise SystemExit(2)
+    if args.steps <= 0 or args.warmup < 0:
+        raise SystemExit("--steps must be positive and --warmup non-negative")
     import torch
 
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
     dev = torch.device("cuda:0")
-    if args.suite:
-        suite(args, dev)
-        return
+    parts = set(p for p in args.parts.split(",") if p)
     if args.copy_probe_mib > 0:
         copy_probe(dev, args.copy_probe_mib)
     log("bench: decode C2")
-    dec = bench_decode(args, dev, [C2_HISTORY], C2_QLEN, pool=193, layers=args.layers)
-    log(f"bench: decode {dec['us_per_layer']:.3f} us/layer ({dec['gbps']:.1f} GB/s)")
+    states = layer_states(dev, [C2_HISTORY], C2_QLEN, 193, args.layers, window=bool(args.window))
+    dec = bench_decode(dev, states, args.steps, args.warmup, tps=args.tps)
+    log(f"bench: decode {dec['us']:.3f} us/layer ({dec['gbps']:.1f} GB/s)")
+    fwd = None
+    if "forward" in parts:
+        fwd = bench_forward(dev, states, args.steps, args.warmup)
+        log(f"bench: forward {fwd['us']:.3f} us/layer")
     qw = None
-    if not args.skip_quant_write:
-        qw = bench_quant_write(args, dev)
-        log(f"bench: quant-write {qw['gbps']:.1f} GB/s")
-    cpu, rel = None, None
-    if not args.no_cpu_baseline:
-        log("bench: cpu baseline + parity gate")
-        cpu, rel = cpu_baseline(dec["state"], dec["out0"], args.cpu_seconds)
-        if not rel <= 1e-3:
-            raise SystemExit(f"decode parity gate failed: rel err {rel:.3e}")
+    if "quant_write" in parts:
+        qw = bench_quant_write(dev)
+        log(f"bench: quant-write {qw['us']:.2f} us, {qw['gbps']:.1f} GB/s")
+    cpu = read_rel = fwd_err = None
+    if "cpu" in parts:
+        log("bench: cpu baseline + parity gates")
+        cpu, read_rel, fwd_ok, fwd_err = cpu_forward_baseline(states[0], dec["out0"],
+                                                               None if fwd is None else fwd["out0"],
+                                                               args.cpu_seconds)
+        if not read_rel <= 1e-3:
+            raise SystemExit(f"decode parity gate failed: rel err {read_rel:.3e}")
+        if fwd_ok is False:
+            raise SystemExit(f"forward parity gate failed: max abs err {fwd_err:.3e}")
+    suite_res = suite(dev, args.suite.split(","), args.suite_cpu_seconds) if "suite" in parts else None
     line = {
         "metric": METRIC,
-        "value": round(dec["us_per_layer"], 4),
+        "value": round(dec["us"], 4),
         "unit": "us/layer",
         "n_gpus": 1,
-        "steps": dec["steps"],
-        "warmup": dec["warmup"],
-        "ms_per_step": dec["us_per_layer"] / 1000.0,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": dec["us"] / 1000.0,
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic",
         "config": {
-            "workload": "C2: MTP decode, 1 request x 4 query tokens, Hq=6 Hk=1 D=256, 24579-token INT2 "
-                        "history in 193 shuffled 128-token pages, FP32 sink=128/recent=256 window "
-                        "(staging 8192), clip 0.96/0.92, int8-geometry caches, 64 distinct layers",
-            "arith": "INT2 dequant to f16, f16 MFMA with f32 accumulation, f32 online softmax",
+            "workload": "C2: MTP decode, 1 request x 4 query tokens, Hq=6 Hk=1 D=256, 24579-token INT2 history in "
+                        "193 shuffled 128-token pages, FP32 sink=128/recent=256 window (staging 8192), clip "
+                        f"0.96/0.92, int8-geometry caches, {args.layers} distinct layers",
+            "arith": "INT2 codes as exact f16 operands, f16 MFMA with f32 accumulation, f32 online softmax",
             "decode_hbm_gbps": round(dec["gbps"], 1),
             "decode_bytes_per_layer": dec["bytes"]["total"],
             "decode_bytes_per_layer_160B_variant": dec["bytes"]["int2_160B_variant"],
             "staged_tokens": dec["bytes"]["staged_tokens"],
-            "decode_parity_rel_err_vs_oracle": rel,
-            "quant_write": None if qw is None else {"workload": "C5 write: 65536 tokens bf16, Hk=1, random slots ~1/16 skipped, "
-                                        "rotation on MFMA, clip 0.96/0.92",
-                            "us_per_call": round(qw["us_per_call"], 3), "gbps": round(qw["gbps"], 1),
-                            "frac_of_hbm_peak": round(qw["gbps"] / HBM_PEAK_GBPS, 4),
-                            "bytes_per_call": qw["bytes"]},
+            "decode_parity_rel_err_vs_oracle": read_rel,
+            "forward": None if fwd is None else {
+                "workload": "the impl forward of the same step per layer: fused step write (q/k/v fp32 rotation, "
+                            "INT2 write and window write of the 4 new tokens), decode, merge with R_v^T and the "
+                            "bf16 cast; bf16 in and out",
+                "us_per_layer": round(fwd["us"], 3), "steps": args.steps, "warmup": args.warmup,
+                "parity_max_abs_err_vs_oracle": fwd_err},
+            "quant_write": None if qw is None else {
+                "workload": "C5 write: 65536 tokens bf16, Hk=1, random slots ~1/16 skipped, rotation on MFMA, "
+                            "clip 0.96/0.92", "steps": qw["steps"],
+                "us_per_call": round(qw["us"], 3), "gbps": round(qw["gbps"], 1),
+                "frac_of_hbm_peak": round(qw["gbps"] / HBM_PEAK_GBPS, 4), "bytes_per_call": qw["bytes"]},
+            "suite": suite_res,
         },
-        "roofline": {"bound": "hbm", "achieved": round(dec["gbps"], 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(dec["gbps"] / HBM_PEAK_GBPS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(dec["gbps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(dec["gbps"] / HBM_PEAK_GBPS, 4),
                      "traffic": traffic_from_profile(ROOT / "oscar_amd" / "csrc" / "paged_decode.hip")},
         "cpu_baseline": cpu,
     }

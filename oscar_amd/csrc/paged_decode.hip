@@ -972,20 +972,26 @@ __global__ __launch_bounds__(256) void paged_decode_merge_small_kernel(DecodeArg
 
 // Merge with the output rotation (the reference's `out @ R_v^T`,
 // backend.py:293-295) and the cast to the model dtype fused in: one
-// 256-thread block per (output row, quarter of the output features) of an
-// item.  The block LSE-combines the row's partials over all 256 rotated
-// features (thread: partial group t / 64, features 4 (t % 64) .. +3), then
-// multiplies the normalised row by its quarter of R_v^T (wave w: rotated
-// features 64w .. 64w + 63 in order, lane: one output feature; the four
-// waves' sums are added in wave order) and writes it as fp32 or bf16 (RNE).
-__global__ __launch_bounds__(256) void paged_decode_merge_rotate_kernel(DecodeArgs a, const float* __restrict__ rot_t,
-                                                                        void* __restrict__ out, int64_t out_stride,
-                                                                        int out_bf16) {
+// 1024-thread block per (output row, quarter of the output features) of an
+// item.  Every load goes out before any wait: the block's 64 columns of R_v^T
+// (wave w: rotated features 16w .. 16w + 15, lane: one output feature), every
+// partial's (m, l) (thread per partial) and the partial rows (wave w: partials
+// w, w + 16, ..., lane: four rotated features).  The block LSE-combines the
+// row over all 256 rotated features, normalises it, multiplies it by its
+// columns of R_v^T (the sixteen waves' sums added in wave order) and writes
+// fp32 or bf16 (RNE).
+constexpr int kRotThreads = 1024;
+constexpr int kRotWaves = kRotThreads / 64;
+constexpr int kRotBatch = 16;                    // partial rows per thread per round
+
+__global__ __launch_bounds__(kRotThreads) void paged_decode_merge_rotate_kernel(
+    DecodeArgs a, const float* __restrict__ rot_t, void* __restrict__ out, int64_t out_stride, int out_bf16) {
   __shared__ float wpart[kMaxPartials];
-  __shared__ float red[2][4];
-  __shared__ floatx4 osum[4][64];
+  __shared__ float red[2][kRotWaves];
+  __shared__ floatx4 osum[kRotWaves][64];
   __shared__ __attribute__((aligned(16))) float orow[kHeadDim];
-  __shared__ float csum[4][64];
+  __shared__ float csum[kRotWaves][64];
+  static_assert(kMaxPartials <= kRotThreads, "one partial per thread");
   const int qd = blockIdx.x & 3;
   const int r = blockIdx.x >> 2;
   const int item = blockIdx.y;
@@ -1003,81 +1009,83 @@ __global__ __launch_bounds__(256) void paged_decode_merge_rotate_kernel(DecodeAr
   const int64_t pstride = (int64_t)a.row_tiles * kPartialFloats;
   auto partial = [&](int p) { return base + (p < hs ? p : a.max_splits) * pstride; };
 
-  // ---- partial weights ----
-  float mreg[kMaxPartials / 256], lreg[kMaxPartials / 256];
-  float mloc = -__builtin_inff();
+  // ---- every load of the first round ----
+  float rv[kHeadDim / kRotWaves];
+  const float* rcol = rot_t + (int64_t)(16 * w) * kHeadDim + 64 * qd + lane;
 #pragma unroll
-  for (int k = 0; k < kMaxPartials / 256; ++k) {
-    const int p = tid + 256 * k;
-    mreg[k] = -__builtin_inff();
-    lreg[k] = 0.f;
-    if (p < P) {
-      mreg[k] = partial(p)[kPartO + r];
-      lreg[k] = partial(p)[kPartO + kRows + r];
-    }
-    mloc = fmaxf(mloc, mreg[k]);
+  for (int k = 0; k < kHeadDim / kRotWaves; ++k) rv[k] = rcol[(int64_t)k * kHeadDim];
+  float mp = -__builtin_inff(), lp = 0.f;
+  if (tid < P) {
+    mp = partial(tid)[kPartO + r];
+    lp = partial(tid)[kPartO + kRows + r];
   }
+  floatx4 x[kRotBatch];
+#pragma unroll
+  for (int k = 0; k < kRotBatch; ++k) {
+    const int p = w + kRotWaves * k;
+    x[k] = p < P ? *reinterpret_cast<const floatx4*>(partial(p) + r * kHeadDim + 4 * lane) : floatx4{};
+  }
+
+  // ---- partial weights ----
+  float mloc = mp;
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, o, 64));
   if (lane == 0) red[0][w] = mloc;
   __syncthreads();
-  const float mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
-  float lsum = 0.f;
+  float mx = red[0][0];
 #pragma unroll
-  for (int k = 0; k < kMaxPartials / 256; ++k) {
-    const int p = tid + 256 * k;
-    if (p < P) {
-      const float wgt = (mreg[k] == -__builtin_inff()) ? 0.f : exp2f(mreg[k] - mx);
-      wpart[p] = wgt;
-      lsum = fmaf(wgt, lreg[k], lsum);
-    }
-  }
+  for (int ww = 1; ww < kRotWaves; ++ww) mx = fmaxf(mx, red[0][ww]);
+  const float wgt = (mp == -__builtin_inff()) ? 0.f : exp2f(mp - mx);
+  if (tid < P) wpart[tid] = wgt;
+  float lsum = wgt * lp;
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) lsum += __shfl_xor(lsum, o, 64);
   if (lane == 0) red[1][w] = lsum;
   __syncthreads();
-  const float L = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+  float L = 0.f;
+#pragma unroll
+  for (int ww = 0; ww < kRotWaves; ++ww) L += red[1][ww];
 
   // ---- the row in the rotated domain ----
   floatx4 acc = floatx4{};
-  constexpr int kBatch = 8;
-  for (int p0 = w; p0 < P; p0 += 4 * kBatch) {
-    floatx4 x[kBatch];
 #pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int p = p0 + 4 * k;
+  for (int k = 0; k < kRotBatch; ++k) {
+    const int p = w + kRotWaves * k;
+    if (p < P) acc += wpart[p] * x[k];
+  }
+  for (int p0 = w + kRotWaves * kRotBatch; p0 < P; p0 += kRotWaves * kRotBatch) {
+#pragma unroll
+    for (int k = 0; k < kRotBatch; ++k) {
+      const int p = p0 + kRotWaves * k;
       x[k] = p < P ? *reinterpret_cast<const floatx4*>(partial(p) + r * kHeadDim + 4 * lane) : floatx4{};
     }
 #pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int p = p0 + 4 * k;
+    for (int k = 0; k < kRotBatch; ++k) {
+      const int p = p0 + kRotWaves * k;
       if (p < P) acc += wpart[p] * x[k];
     }
   }
   osum[w][lane] = acc;
   __syncthreads();
   if (w == 0) {
+    floatx4 o = osum[0][lane];
+#pragma unroll
+    for (int ww = 1; ww < kRotWaves; ++ww) o += osum[ww][lane];
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    const floatx4 o = ((osum[0][lane] + osum[1][lane]) + osum[2][lane]) + osum[3][lane];
     *reinterpret_cast<floatx4*>(&orow[4 * lane]) = o * inv;
   }
   __syncthreads();
 
   // ---- out[64 qd + lane] = sum_f orow[f] * R_v^T[f][64 qd + lane] ----
-  const float* rt_col = rot_t + (int64_t)(64 * w) * kHeadDim + 64 * qd + lane;
   float y = 0.f;
 #pragma unroll
-  for (int f0 = 0; f0 < 64; f0 += 16) {
-    float rv[16];
-#pragma unroll
-    for (int k = 0; k < 16; ++k) rv[k] = rt_col[(int64_t)(f0 + k) * kHeadDim];
-#pragma unroll
-    for (int k = 0; k < 16; ++k) y = fmaf(orow[64 * w + f0 + k], rv[k], y);
-  }
+  for (int k = 0; k < kHeadDim / kRotWaves; ++k) y = fmaf(orow[16 * w + k], rv[k], y);
   csum[w][lane] = y;
   __syncthreads();
   if (w == 0) {
-    const float o = ((csum[0][lane] + csum[1][lane]) + csum[2][lane]) + csum[3][lane];
+    float o = csum[0][lane];
+#pragma unroll
+    for (int ww = 1; ww < kRotWaves; ++ww) o += csum[ww][lane];
     const int j = row / a.group;
     const int h = it.kvh * a.group + (row - j * a.group);
     const int64_t idx = (int64_t)(it.qa + j) * out_stride + (int64_t)h * kHeadDim + 64 * qd + lane;
@@ -1265,7 +1273,7 @@ int launch_merge(const DecodeArgs& a, int64_t max_rows, unsigned nitems, const O
   const int mr = merge_rows(max_rows);
   if (orot.rot_t != nullptr) {
     dim3 grid((unsigned)(mr * 4), nitems, (unsigned)a.row_tiles);
-    hipLaunchKernelGGL(paged_decode_merge_rotate_kernel, grid, dim3(256), 0, stream, a, orot.rot_t, orot.out,
+    hipLaunchKernelGGL(paged_decode_merge_rotate_kernel, grid, dim3(kRotThreads), 0, stream, a, orot.rot_t, orot.out,
                        orot.out_stride, (int)orot.out_bf16);
   } else if (a.max_splits + a.fresh <= kSmallP) {
     dim3 grid((unsigned)((mr * 4 + 15) / 16), nitems, (unsigned)a.row_tiles);
