@@ -11,6 +11,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace oscar {
 
 constexpr int kHeadDim = 256;          // the kernels are written for D = 256
@@ -35,6 +37,18 @@ enum Status : int {
   kErrLaunch = -4,
   kErrUnsupportedGeometry = -5,
 };
+
+// hipFuncSetAttribute(MaxDynamicSharedMemorySize) once per (kernel, device):
+// `done` holds one bit per device ordinal (ordinals >= 64 set it on every call).
+inline int set_dynamic_lds(const void* kernel, int bytes, std::atomic<uint64_t>& done) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return kErrLaunch;
+  const uint64_t bit = dev < 64 ? (1ull << dev) : 0ull;
+  if (bit != 0ull && (done.load(std::memory_order_acquire) & bit) != 0ull) return kOk;
+  if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) return kErrLaunch;
+  done.fetch_or(bit, std::memory_order_acq_rel);
+  return kOk;
+}
 
 // Division of n in [0, 2^31) by a divisor d in [1, 2^31) fixed at launch, as
 // a multiply-high, an add and a shift (Granlund and Montgomery, "Division by

@@ -1244,15 +1244,10 @@ int fill_common(DecodeArgs& a, const float* q_rot, int32_t num_heads, int32_t nu
   return kOk;
 }
 
+std::atomic<uint64_t> g_split_lds_set{0};
+
 int set_split_lds() {
-  static bool lds_attr_set = false;
-  if (!lds_attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(paged_decode_split_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes) != hipSuccess)
-      return kErrLaunch;
-    lds_attr_set = true;
-  }
-  return kOk;
+  return set_dynamic_lds(reinterpret_cast<const void*>(paged_decode_split_kernel), (int)kLdsBytes, g_split_lds_set);
 }
 
 // Merge blocks per feature quarter: one per row of a row tile that can hold

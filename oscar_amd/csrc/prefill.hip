@@ -602,6 +602,8 @@ __global__ __launch_bounds__(512, 1) void prefill_kernel(PrefillArgs a) {
   }
 }
 
+std::atomic<uint64_t> g_lds_set{0};   // dynamic-LDS attribute set, one bit per device
+
 }  // namespace
 }  // namespace oscar
 
@@ -661,13 +663,7 @@ extern "C" int oscar_prefill_continuation(
   a.out = out;
   const int64_t rows = (int64_t)num_new * a.group;
   dim3 grid((unsigned)((rows + kWaves * kRowsPerWave - 1) / (kWaves * kRowsPerWave)), (unsigned)num_kv_heads);
-  static bool lds_attr_set = false;
-  if (!lds_attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPrefillLds) != hipSuccess)
-      return kErrLaunch;
-    lds_attr_set = true;
-  }
+  if (set_dynamic_lds(reinterpret_cast<const void*>(prefill_kernel), (int)kPrefillLds, g_lds_set) != kOk) return kErrLaunch;
   hipLaunchKernelGGL(prefill_kernel, grid, dim3(2 * kWaves * 64), kPrefillLds, stream, a);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }

@@ -445,6 +445,8 @@ int check_cache_args(const CacheArgs& c) {
   return kOk;
 }
 
+std::atomic<uint64_t> g_lds_set{0};   // dynamic-LDS attribute set, one bit per device
+
 }  // namespace
 }  // namespace oscar
 
@@ -518,13 +520,7 @@ int oscar_quant_write(const void* key_bf16, const void* value_bf16, int64_t num_
               block_size, num_pages * (int64_t)block_size};
   int st = check_cache_args(c);
   if (st != kOk) return st;
-  static bool lds_attr_set = false;
-  if (!lds_attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(quant_write_fused_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kFusedLds) != hipSuccess)
-      return kErrLaunch;
-    lds_attr_set = true;
-  }
+  if (set_dynamic_lds(reinterpret_cast<const void*>(quant_write_fused_kernel), (int)kFusedLds, g_lds_set) != kOk) return kErrLaunch;
   const int64_t per_block = kFusedWaves * kTokPerWave;
   dim3 grid((unsigned)((num_tokens + per_block - 1) / per_block), (unsigned)(num_kv_heads * 2));
   // The second workgroup of each CU is held back when the grid fills the GPU
