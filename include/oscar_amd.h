@@ -146,6 +146,30 @@ int oscar_paged_decode_rotated(const float* q_rot, const float* k_new, const flo
                                int64_t out_token_stride, int32_t out_bf16, void* workspace,
                                size_t workspace_size, oscar_stream_t stream);
 
+/* The same decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  This entry has no counterpart in the
+ * reference.  The split partials live in a file-scope device array of the
+ * library, 32 MiB per GPU (held until the process ends); a launch whose
+ * partials need more (oscar_paged_decode_workspace_bytes with the same
+ * arguments) returns OSCAR_ERR_WORKSPACE_TOO_SMALL and enqueues nothing.  The
+ * entry allocates nothing and needs no zeroed memory.  Calls that overlap on
+ * one GPU (several streams) share the array and race; the array keeps the
+ * last call's partials.  Arguments as oscar_paged_decode.
+ */
+int oscar_paged_decode_noalloc(const float* q_rot, const float* k_new, const float* v_new,
+                               int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                               int32_t head_size, const void* k_cache, const void* v_cache,
+                               int32_t block_size, int64_t num_pages, int64_t k_stride_page,
+                               int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
+                               int64_t v_stride_token, int64_t v_stride_head, const int32_t* block_table,
+                               int64_t block_table_stride, int32_t block_table_cols,
+                               const int32_t* query_start_loc, const int32_t* seq_lens,
+                               int32_t num_requests, int32_t max_query_len, int64_t max_history,
+                               const int64_t* stage_owner, const void* stage_k_image,
+                               const void* stage_v_image, int32_t stage_rows, float scale,
+                               int32_t tiles_per_split, float* out, oscar_stream_t stream);
+
 /* ---------------------------------------------------------------- DecodeOnly decode
  * One query token per request over its whole history [0, seq_lens[i]) when
  * the step brings no fresh K/V (key = None).  Replaces

@@ -1374,6 +1374,37 @@ int paged_decode(const float* q_rot, const float* k_new, const float* v_new, int
   return kOk;
 }
 
+// Device scratch of the no-allocation entry (oscar_paged_decode_noalloc):
+// the split partials of one launch, at most kScratchBytes.  Every GPU the
+// library runs on holds its own copy until the process ends.
+constexpr size_t kScratchBytes = size_t(32) << 20;
+
+}  // namespace
+}  // namespace oscar
+
+static __device__ __align__(256) uint8_t scratch[oscar::kScratchBytes];
+
+namespace oscar {
+namespace {
+
+// Device address of this GPU's `scratch`, looked up once per device with
+// that device current (the array's name is a host-side stand-in, never a
+// device address).
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_addr[kMaxDevices];
+
+int scratch_address(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return kErrLaunch;
+  void* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return kErrLaunch;
+    g_scratch_addr[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return kOk;
+}
+
 }  // namespace
 }  // namespace oscar
 
@@ -1426,6 +1457,31 @@ int oscar_paged_decode_rotated(const float* q_rot, const float* k_new, const flo
                       stage_k_image, stage_v_image, stage_rows, scale, tiles_per_split,
                       reinterpret_cast<float*>(out), OutRotation{rot_v_t, out, out_token_stride, out_bf16},
                       workspace, workspace_size, stream);
+}
+
+int oscar_paged_decode_noalloc(const float* q_rot, const float* k_new, const float* v_new,
+                               int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                               int32_t head_size, const void* k_cache, const void* v_cache,
+                               int32_t block_size, int64_t num_pages, int64_t k_stride_page,
+                               int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
+                               int64_t v_stride_token, int64_t v_stride_head, const int32_t* block_table,
+                               int64_t block_table_stride, int32_t block_table_cols,
+                               const int32_t* query_start_loc, const int32_t* seq_lens,
+                               int32_t num_requests, int32_t max_query_len, int64_t max_history,
+                               const int64_t* stage_owner, const void* stage_k_image,
+                               const void* stage_v_image, int32_t stage_rows, float scale,
+                               int32_t tiles_per_split, float* out, hipStream_t stream) {
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != kOk) return rc;
+  // oscar_paged_decode rejects a launch whose partials exceed the scratch
+  // (kErrWorkspaceTooSmall) before anything is enqueued.
+  return oscar_paged_decode(q_rot, k_new, v_new, num_tokens, num_heads, num_kv_heads, head_size, k_cache, v_cache,
+                            block_size, num_pages, k_stride_page, k_stride_token, k_stride_head, v_stride_page,
+                            v_stride_token, v_stride_head, block_table, block_table_stride, block_table_cols,
+                            query_start_loc, seq_lens, num_requests, max_query_len, max_history, stage_owner,
+                            stage_k_image, stage_v_image, stage_rows, scale, tiles_per_split, out, ws, kScratchBytes,
+                            stream);
 }
 
 size_t oscar_decode_only_workspace_bytes(int32_t num_requests, int32_t num_kv_heads, int32_t num_heads,

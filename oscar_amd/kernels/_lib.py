@@ -35,6 +35,10 @@ SIGNATURES = {
                                     _c_p, _c_i64, _c_i32, _c_p, _c_p, _c_i32, _c_i32, _c_i64,
                                     _c_p, _c_p, _c_p, _c_i32, _c_f32, _c_i32, _c_p, _c_p, _c_sz,
                                     _c_p]),
+    "oscar_paged_decode_noalloc": (_c_i32, [_c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_p,
+                                            _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                            _c_p, _c_i64, _c_i32, _c_p, _c_p, _c_i32, _c_i32, _c_i64,
+                                            _c_p, _c_p, _c_p, _c_i32, _c_f32, _c_i32, _c_p, _c_p]),
     "oscar_paged_decode_rotated": (_c_i32, [_c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_p,
                                             _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                             _c_p, _c_i64, _c_i32, _c_p, _c_p, _c_i32, _c_i32, _c_i64,
