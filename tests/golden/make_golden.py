@@ -11,6 +11,12 @@ seeded inputs (D = 32 so each fixture stays under 100 KB):
   each step of multi-request writes with hash collisions, padding requests,
   skipped slots and recycled pages (AscendOscarAttentionBackendImpl
   ._ensure_staging / _staging_write, oscar_ascend/backend.py:418-481);
+* decode_only_*.npz — the windowed DecodeOnly read
+  (_decode_attention_windowed, oscar_ascend/backend.py:500-586): INT2 middle,
+  FP32 sink when fully staged, the staged run ending at the last position,
+  merged by log-sum-exp, on arenas with planted gaps (an unstaged sink seat,
+  unstaged positions inside the recent window, a request no longer than the
+  sink, seat collisions);
 * forward_*.npz — the impl-level forward (rotate + clip + INT2 store +
   staging + read, backend.py:150-415) for a prefill step followed by MTP
   steps, through the default dense route and through the paged route (its
@@ -136,6 +142,58 @@ def forward_case(backend, paged, name, route, window, clip, seed, d=32, hk=1, hq
     np.savez_compressed(OUT / f"forward_{name}.npz", **rec)
 
 
+def decode_only_case(backend, name, seed, d=32, hk=1, hq=4, bs=16, pool=40, sink=16, recent=32, staging=64):
+    """History written by the reference's own store + window write, gaps planted in
+    the owner tags, then the windowed DecodeOnly read."""
+    g = torch.Generator().manual_seed(seed)
+    impl = make_impl(backend, d, hk, hq, sink, recent, staging)
+    impl._oscar_use_triton = False
+    import oscar_ascend.kernels.store_kernel as store
+
+    store.oscar_store_triton = store.oscar_store_ref
+    rk = torch.linalg.qr(torch.randn(d, d, generator=g)).Q
+    rv = torch.linalg.qr(torch.randn(d, d, generator=g)).Q
+    layer = NS(layer_name="model.layers.0.self_attn.attn", _oscar_rots=(rk, rv))
+    cache = [torch.zeros(pool, bs, hk, d, dtype=torch.bfloat16) for _ in range(2)]
+    perm = torch.randperm(pool, generator=g).to(torch.int32)
+    seqs = [70, 9, 45, 100]
+    per = pool // len(seqs)
+    bt = torch.stack([perm[i * per:(i + 1) * per] for i in range(len(seqs))])
+    qsl, slots = [0], []
+    for r, s in enumerate(seqs):
+        qsl.append(qsl[-1] + s)
+        pos = torch.arange(s)
+        slots += (bt[r][pos // bs].long() * bs + pos % bs).tolist()
+    n = sum(seqs)
+    k = torch.randn(n, hk, d, generator=g) * torch.linspace(0.5, 3.0, d)
+    v = torch.randn(n, hk, d, generator=g)
+    md = meta(slots, qsl, seqs, bt)
+    impl._set_caches(cache)
+    impl._ensure_staging(layer, cache)
+    impl.do_kv_cache_update(layer, k, v, cache, md.slot_mapping)
+    impl._staging_write(layer, k, v, md)
+    owner = layer._oscar_slot_owner
+    R = layer._oscar_stage_rows
+
+    def unstage(r, pos):
+        page = int(bt[r][pos // bs])
+        owner[page % R, pos % bs] = -1
+
+    unstage(0, 3)                     # request 0: a sink seat lost -> no sink segment
+    unstage(2, seqs[2] - 4)           # request 2: the staged tail run starts after this gap
+    unstage(3, seqs[3] - 1)           # request 3: last position unstaged -> no tail segment
+    q = torch.randn(len(seqs), hq, d, generator=g)
+    dmd = NS(seq_lens=torch.tensor(seqs), block_tables=bt)
+    out = impl._decode_attention(q, cache, dmd, layer)
+    rec = {"d": d, "hk": hk, "hq": hq, "bs": bs, "sink": sink, "recent": recent, "staging": staging,
+           "rk": rk.numpy(), "rv": rv.numpy(), "bt": bt.numpy(), "seqs": np.asarray(seqs, dtype=np.int64),
+           "q": q.numpy(), "out": out.numpy().copy(), "kcache": cache[0].view(torch.uint8).numpy().copy(),
+           "vcache": cache[1].view(torch.uint8).numpy().copy(), "owner": owner.numpy().copy(),
+           "stage_k": layer._oscar_stage_k.numpy().copy(), "stage_v": layer._oscar_stage_v.numpy().copy(),
+           "sink_eff": impl.sink_eff}
+    np.savez_compressed(OUT / f"decode_only_{name}.npz", **rec)
+
+
 def main():
     backend, paged = ref_modules()
     torch.set_num_threads(4)
@@ -160,6 +218,8 @@ def main():
             for clip in ((0.0, 0.0), (0.96, 0.92)):
                 tag = f"{route}_w{int(window)}_c{int(clip[0] > 0)}"
                 forward_case(backend, paged, tag, route, window, clip, seed=21)
+    decode_only_case(backend, "gaps", seed=31)
+    decode_only_case(backend, "bs8", seed=32, bs=8, pool=64, sink=8, recent=24, staging=32)
     print("golden fixtures written to", OUT)
 
 

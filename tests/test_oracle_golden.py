@@ -10,7 +10,12 @@ reference's own AscendOscarAttentionBackendImpl (oscar_ascend/backend.py):
 * forward_*.npz — the impl-level forward (rotate + clip + INT2 store + window +
   read, backend.py:150-415) over a prefill step and three MTP steps, through
   the reference's default dense route and its paged route, with and without
-  the window and clipping, plus the INT2 cache bytes after the last step.
+  the window and clipping, plus the INT2 cache bytes after the last step;
+* decode_only_*.npz — the windowed DecodeOnly read (backend.py:500-586) on
+  arenas with planted gaps: a lost sink seat, an unstaged position inside the
+  recent window, an unstaged last position, a request no longer than the
+  sink.  The oracle's window bounds and LSE merge are replayed on the same
+  caches and arena.
 
 Tolerances: owner tags and INT2 cache bytes are compared bit-exactly; staged
 fp32 vectors and attention outputs (fp32 on both sides, different summation
@@ -83,3 +88,31 @@ def test_forward_matches_reference(name):
                                    err_msg=f"{name} step {i}")
     assert np.array_equal(kc.view(torch.uint8).numpy(), z["kcache"]), "K cache bytes differ"
     assert np.array_equal(vc.view(torch.uint8).numpy(), z["vcache"]), "V cache bytes differ"
+
+
+@pytest.mark.parametrize("name", ["decode_only_gaps.npz", "decode_only_bs8.npz"])
+def test_decode_only_windowed_matches_reference(name):
+    from oracle import attention as oatt
+
+    z = load(name)
+    d, hk, bs = int(z["d"]), int(z["hk"]), int(z["bs"])
+    kc = torch.from_numpy(z["kcache"]).view(torch.bfloat16).view(-1, bs, hk, d)
+    vc = torch.from_numpy(z["vcache"]).view(torch.bfloat16).view(-1, bs, hk, d)
+    rk, rv = torch.from_numpy(z["rk"]), torch.from_numpy(z["rv"])
+    q = torch.from_numpy(z["q"])
+    seqs = [int(x) for x in z["seqs"]]
+    arena = (torch.from_numpy(z["stage_k"]), torch.from_numpy(z["stage_v"]), torch.from_numpy(z["owner"]),
+             int(z["sink_eff"]), int(z["recent"]))
+    got = oatt.decode_only_ref(q.float() @ rk, kc, vc, torch.from_numpy(z["bt"]), seqs, d ** -0.5, hk, d,
+                               arena) @ rv.t()
+    want = torch.from_numpy(z["out"])
+    assert (got - want).abs().max().item() <= FP32_ABS
+    # A plausible misreading, taking the staged value wherever the owner tag
+    # matches (the MTP read's rule), does not reproduce the reference here.
+    naive = torch.zeros_like(want)
+    for b, seq in enumerate(seqs):
+        hk_, hv_ = oatt.history(kc, vc, torch.from_numpy(z["bt"])[b], seq, hk, d, arena[:3])
+        qr = (q[b].float() @ rk).view(hk, -1, d)                     # [Hk, group, D]
+        p = torch.softmax(torch.einsum("kgd,tkd->kgt", qr, hk_) * d ** -0.5, -1)
+        naive[b] = torch.einsum("kgt,tkd->kgd", p, hv_).reshape(-1, d) @ rv.t()
+    assert (naive - want).abs().max().item() > 1e-3
