@@ -189,9 +189,10 @@ class OscarAttentionBackendImpl:
         # fp16 operand images of the window for the paged decode (32-token tiles)
         layer._oscar_stage_kimg = layer._oscar_stage_vimg = None
         if bs % 32 == 0:
-            shape = staging.image_shape(rows, bs, self.num_kv_heads)
-            layer._oscar_stage_kimg = torch.zeros(shape, dtype=torch.float16, device=dev)
-            layer._oscar_stage_vimg = torch.zeros(shape, dtype=torch.float16, device=dev)
+            layer._oscar_stage_kimg = torch.zeros(staging.k_image_shape(rows, bs, self.num_kv_heads),
+                                                  dtype=torch.float16, device=dev)
+            layer._oscar_stage_vimg = torch.zeros(staging.image_shape(rows, bs, self.num_kv_heads),
+                                                  dtype=torch.float16, device=dev)
         layer._oscar_stage_rows = rows
         layer._oscar_stage_ready = True
         self._oscar_stage_ready = True

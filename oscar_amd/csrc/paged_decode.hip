@@ -59,6 +59,7 @@
 // else 0; cut starts the run of staged positions that ends at seq - 1 inside
 // [max(seq - recent, head), seq).
 #include "oscar_common.h"
+#include "window_images.h"
 
 namespace oscar {
 namespace {
@@ -70,7 +71,6 @@ constexpr int kStepTok = kWaves * kTile;  // history tokens per step: one tile p
 constexpr int kMaxFresh = 16;
 constexpr int kPRow = 40;               // halves per P' row: 32 token slots + pad (16-byte rows)
 constexpr int kVtRow = 10;              // dwords per V code byte row: 8 groups of 4 tokens + pad
-constexpr int kImgHalfs = 16 * 64 * 8;  // one staged operand image: 16 blocks x 64 lanes x 8
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 4.f;            // log2 headroom before a running max is raised
 constexpr float kLazyVsMax = 4094.f;    // 16 * 4094 < 65504 (fp16 max)
@@ -108,7 +108,7 @@ struct DecodeArgs {
   int32_t bt_cols;
   int32_t num_heads, num_kv_heads, group;
   const int64_t* owner;         // [rows, bs] or null
-  const _Float16* kimg;         // [rows][bs / 32][Hk][kImgHalfs]
+  const _Float16* kimg;         // [rows][bs / 32][Hk][kKImgHalfs]
   const _Float16* vimg;
   int32_t stage_rows;
   float scale_log2;             // attention scale * log2(e)
@@ -120,24 +120,29 @@ struct DecodeArgs {
   ItemInfo items[kMaxInlineItems];
 };
 
-// One step is 128 history tokens, one 32-token tile per wavefront.  Its
-// exchange buffers are double-buffered across steps.
+// One step is 128 history tokens, one 32-token tile per wavefront.  Only the
+// V code transpose is written before a step's first barrier, while a slower
+// wave may still run the previous step's PV pass on it, so it alone is
+// double-buffered; everything else a step exchanges is written after that
+// barrier and read before the next step's.
 struct StepLds {
-  _Float16 p[kWaves][kRows * kPRow];       // P' = p * vs of each tile's INT2 tokens, [row][slot]
-  _Float16 pw[kWaves][kRows * kPRow];      // p / 4 of each tile's window tokens, [row][slot]
   uint32_t vt[kWaves][64 * kVtRow];        // V code bytes, [byte][group of 4 tokens]
-  float mx[kWaves][kRows];                 // each tile's row maxima
-  uint32_t big[kWaves];                    // the tile holds a V scale above kLazyVsMax
 };
 
 struct MainLds {
-  _Float16 q[16 * 2 * kRows * 8];          // Q^T operand [m][g][row][8]
-  float qsum[kRows];                       // sum of each row's fp16 q
+  _Float16 q[16 * 2 * kRows * 8];          // Q^T operand [m][g][row][8], fp16 high part
+  _Float16 qlo[16 * 2 * kRows * 8];        // the low part, fp16(q - high): q = high + low to 2^-22
+  float qsum[kRows];                       // sum of each row's q
   float ta[kWaves][kTile];                 // score = ta * acc + tb * qsum + tm (own tile)
   float tb[kWaves][kTile];
   float tm[kWaves][kTile];                 // 0, or -inf for a token left out
   float tvs[kWaves][kTile];                // V scale of an INT2 token (else 0)
-  float tvz[kWaves][kTile];                // V zero of an INT2 token (else 0)
+  float trv[kWaves][kTile];                // 1 / V scale of an INT2 token (else 0)
+  float tvz[kWaves][kTile];                // V zero / V scale of an INT2 token (else 0)
+  _Float16 p[kWaves][kRows * kPRow];       // P' = p * vs of each tile's INT2 tokens, [row][slot]
+  _Float16 pw[kWaves][kRows * kPRow];      // p / 4 of each tile's window tokens, [row][slot]
+  float mx[kWaves][kRows];                 // each tile's row maxima
+  uint32_t big[kWaves];                    // the tile holds a V scale above kLazyVsMax
   StepLds buf[2];
 };
 
@@ -471,7 +476,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   }
   StepLoad cur = load_step(a, pg, split * kStepTok, prefix, kvh, w, lane);
 
-  // ---- Q^T operand into LDS (permuted K dimension, fp16) and row sums ----
+  // ---- Q^T operand into LDS (permuted K dimension, fp16 high + low parts) and row sums ----
   // Thread: row r8, features 32 * c8 .. +31, which are exactly the four
   // operand vectors (m = 2jj + aa, gg) with jj = 2(c8 & 3) + jl: slot 2i + b of
   // vector (jl, aa) is local feature 16jl + 4aa + i + 8b.
@@ -482,15 +487,18 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
     for (int jl = 0; jl < 2; ++jl) {
 #pragma unroll
       for (int aa = 0; aa < 2; ++aa) {
-        half8 v;
+        half8 v, vl;
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           const int k = 16 * jl + 4 * aa + (u >> 1) + 8 * (u & 1);
-          v[u] = (_Float16)x[k >> 2][k & 3];
-          qs += (float)v[u];
+          const float xq = x[k >> 2][k & 3];
+          v[u] = (_Float16)xq;
+          vl[u] = (_Float16)(xq - (float)v[u]);
+          qs += xq;
         }
         const int m = 2 * (2 * (c8 & 3) + jl) + aa;
         *reinterpret_cast<half8*>(&S.q[((m * 2 + gg) * kRows + r8) * 8]) = v;
+        *reinterpret_cast<half8*>(&S.qlo[((m * 2 + gg) * kRows + r8) * 8]) = vl;
       }
     }
     qs += shfl_xor_f32(qs, 1);
@@ -537,7 +545,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
     // image now, a phase before the score pass uses it (the second half goes
     // out at the start of that pass).
     const u32x4* img = reinterpret_cast<const u32x4*>(
-        a.kimg + image_index(a, wmw != 0u ? pgw : 0, (int)fast_mod((uint32_t)p0, a.bs_div), kvh) * kImgHalfs);
+        a.kimg + image_index(a, wmw != 0u ? pgw : 0, (int)fast_mod((uint32_t)p0, a.bs_div), kvh) * kKImgHalfs);
     u32x4 im[16];
     if (wmw != 0u) {
 #pragma unroll
@@ -557,8 +565,10 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
         S.ta[w][col] = used ? 4.f * ksc * a.scale_log2 : (win ? a.scale_log2 : 0.f);
         S.tb[w][col] = used ? (kz - 4.f * ksc) * a.scale_log2 : 0.f;
         S.tm[w][col] = (used || win) ? 0.f : -__builtin_inff();
+        const float rvs = used ? 1.f / vsc : 0.f;
         S.tvs[w][col] = used ? vsc : 0.f;
-        S.tvz[w][col] = used ? vz : 0.f;
+        S.trv[w][col] = rvs;
+        S.tvz[w][col] = used ? vz * rvs : 0.f;
       }
       big = __ballot(used && vsc > kLazyVsMax) != 0;
       const int tq = lane & 7, bg = lane >> 3;
@@ -576,23 +586,32 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
     // ---- S^T = K Q^T of the own tile (window tokens from their image) ----
     floatx16 s;
     {
-      // Q^T operands are read from LDS one k-step pair ahead of their use.
+      // Q^T operands (high and low parts, so the products see q to 2^-22;
+      // the code operands 1 + c/4 are exact) are read from LDS one k-step
+      // pair ahead of their use.
       const half8* qsrc = reinterpret_cast<const half8*>(&S.q[(g * kRows + col) * 8]);   // + m * 2 * kRows
+      const half8* qlsrc = reinterpret_cast<const half8*>(&S.qlo[(g * kRows + col) * 8]);
       const uint32_t kw[8] = {L.kc0[0], L.kc0[1], L.kc0[2], L.kc0[3], L.kc1[0], L.kc1[1], L.kc1[2], L.kc1[3]};
       // One accumulator chain: the other workgroup on the SIMD covers the
       // MFMA latency.
       s = floatx16{};
-      half8 qa = qsrc[0], qb = qsrc[2 * kRows];
+      half8 qa = qsrc[0], qb = qsrc[2 * kRows], qal = qlsrc[0], qbl = qlsrc[2 * kRows];
       auto qk_pair = [&](int j, const half8& k0, const half8& k1) {
-        half8 na = qa, nb = qb;
+        half8 na = qa, nb = qb, nal = qal, nbl = qbl;
         if (j < 7) {
           na = qsrc[(2 * j + 2) * 2 * kRows];
           nb = qsrc[(2 * j + 3) * 2 * kRows];
+          nal = qlsrc[(2 * j + 2) * 2 * kRows];
+          nbl = qlsrc[(2 * j + 3) * 2 * kRows];
         }
         s = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qa, s, 0, 0, 0);
         s = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qb, s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qal, s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qbl, s, 0, 0, 0);
         qa = na;
         qb = nb;
+        qal = nal;
+        qbl = nbl;
       };
       if (wmw == 0u) {
 #pragma unroll
@@ -605,6 +624,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
 #pragma unroll
         for (int m = 8; m < 16; ++m) im[m] = img[m * 64 + lane];
         const bool wl = (wmw >> col) & 1u;
+        const u32x4* img_lo = img + 16 * 64;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           half8 ka[2];
@@ -613,6 +633,26 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
           for (int aa = 0; aa < 2; ++aa)
             ka[aa] = wl ? __builtin_bit_cast(half8, im[2 * j + aa]) : ka[aa];
           qk_pair(j, ka[0], ka[1]);
+          // Once a half of the high part is used, its registers take the same
+          // half of the low part, zero for lanes of tokens outside the window
+          // (the barriers keep the loads from moving up, where they would
+          // need registers of their own).
+          if (j == 3 || j == 7) {
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int m = 0; m < 8; ++m) im[m + (j - 3) * 2] = wl ? img_lo[(m + (j - 3) * 2) * 64 + lane] : u32x4{};
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+        // window tokens (the other lanes hold zeros): low part of k against
+        // the high part of q (the low-low product is below 2^-22 of the
+        // score's terms)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const half8 la = __builtin_bit_cast(half8, im[2 * j]);
+          const half8 lb = __builtin_bit_cast(half8, im[2 * j + 1]);
+          s = __builtin_amdgcn_mfma_f32_32x32x16_f16(la, qsrc[(2 * j) * 2 * kRows], s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_32x32x16_f16(lb, qsrc[(2 * j + 1) * 2 * kRows], s, 0, 0, 0);
         }
       }
     }
@@ -649,14 +689,14 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
       }
     }
     mb = fmaxf(mb, shfl_xor_f32(mb, 32));
-    if (g == 0) B.mx[w][col] = mb;
-    if (lane == 0) B.big[w] = big ? 1u : 0u;
+    if (g == 0) S.mx[w][col] = mb;
+    if (lane == 0) S.big[w] = big ? 1u : 0u;
     lds_barrier();
 
     // ---- common max of the step (same decision in every wave), P' of the own tile ----
     {
-      const float M = fmaxf(fmaxf(B.mx[0][col], B.mx[1][col]), fmaxf(B.mx[2][col], B.mx[3][col]));
-      const bool eager = (B.big[0] | B.big[1] | B.big[2] | B.big[3]) != 0u;
+      const float M = fmaxf(fmaxf(S.mx[0][col], S.mx[1][col]), fmaxf(S.mx[2][col], S.mx[3][col]));
+      const bool eager = (S.big[0] | S.big[1] | S.big[2] | S.big[3]) != 0u;
       const bool need = M > m_run + (eager ? 0.f : kLazy);
       const bool resc = need && m_run != -__builtin_inff();
       if (__ballot(resc)) {
@@ -674,25 +714,32 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
       const float m_use = m_run == -__builtin_inff() ? 0.f : m_run;
       float psum = 0.f, zsum = 0.f, pss = 0.f;
       const half2v ones{(_Float16)1.f, (_Float16)1.f};
-      _Float16* prow = &B.p[w][col * kPRow + 4 * g];
-      _Float16* pwrow = &B.pw[w][col * kPRow + 4 * g];
+      _Float16* prow = &S.p[w][col * kPRow + 4 * g];
+      _Float16* pwrow = &S.pw[w][col * kPRow + 4 * g];
 #pragma unroll
+      // The row sums take each token's weight as the PV pass sees it (after
+      // its fp16 rounding: P' / vs of an INT2 token, 4 * (p / 4) of a window
+      // token), so that the output is a convex combination of the values
+      // whatever that rounding did.
       for (int jj = 0; jj < 4; ++jj) {
         const floatx4 vsv = *reinterpret_cast<const floatx4*>(&S.tvs[w][8 * jj + 4 * g]);
-        const floatx4 vze = *reinterpret_cast<const floatx4*>(&S.tvz[w][8 * jj + 4 * g]);
+        const floatx4 rvv = *reinterpret_cast<const floatx4*>(&S.trv[w][8 * jj + 4 * g]);
+        const floatx4 zrv = *reinterpret_cast<const floatx4*>(&S.tvz[w][8 * jj + 4 * g]);
         float p[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p[i] = exp2_raw(s[4 * jj + i] - m_use);
-          psum += p[i];
-          zsum = fmaf(p[i], vze[i], zsum);
-        }
+        for (int i = 0; i < 4; ++i) p[i] = exp2_raw(s[4 * jj + i] - m_use);
         // slots 8jj + 4g + {0, 1, 2, 3} hold tokens 8jj + 4g + {0, 2, 1, 3}
         const half4 h = half4{(_Float16)(p[0] * vsv[0]), (_Float16)(p[2] * vsv[2]), (_Float16)(p[1] * vsv[1]),
                               (_Float16)(p[3] * vsv[3])};
         *reinterpret_cast<half4*>(prow + 8 * jj) = h;
         pss = __builtin_amdgcn_fdot2(half2v{h[0], h[1]}, ones, pss, false);
         pss = __builtin_amdgcn_fdot2(half2v{h[2], h[3]}, ones, pss, false);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float wi = (float)h[i == 1 ? 2 : (i == 2 ? 1 : i)];
+          psum = fmaf(wi, rvv[i], psum);
+          zsum = fmaf(wi, zrv[i], zsum);
+        }
         if (wmw != 0u) {
           const uint32_t wb = wmw >> (8 * jj + 4 * g);
           const half4 hw = half4{(wb & 1u) ? (_Float16)(0.25f * p[0]) : (_Float16)0.f,
@@ -700,6 +747,9 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
                                  (wb & 2u) ? (_Float16)(0.25f * p[1]) : (_Float16)0.f,
                                  (wb & 8u) ? (_Float16)(0.25f * p[3]) : (_Float16)0.f};
           *reinterpret_cast<half4*>(pwrow + 8 * jj) = hw;
+          float ws = __builtin_amdgcn_fdot2(half2v{hw[0], hw[1]}, ones, 0.f, false);
+          ws = __builtin_amdgcn_fdot2(half2v{hw[2], hw[3]}, ones, ws, false);
+          psum = fmaf(4.f, ws, psum);
         }
       }
       l_run += psum;
@@ -713,7 +763,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
     for (int j = 0; j < kWaves; ++j) {
       if (pgs[j] < 0 || tbase + kTile * j >= prefix) continue;
       const uint32_t* vr = &B.vt[j][vrow * kVtRow];
-      const _Float16* pr = &B.p[j][col * kPRow + 8 * g];
+      const _Float16* pr = &S.p[j][col * kPRow + 8 * g];
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
         const uint32_t d0 = vr[4 * s2 + 2 * g], d1 = vr[4 * s2 + 2 * g + 1];
@@ -727,7 +777,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
       }
       const uint32_t wmj = j == 0 ? wm0 : (j == 1 ? wm1 : (j == 2 ? wm2 : wm3));
       if (wmj != 0u) {
-        const _Float16* pwr = &B.pw[j][col * kPRow + 8 * g];
+        const _Float16* pwr = &S.pw[j][col * kPRow + 8 * g];
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
           const half8 pwop = *reinterpret_cast<const half8*>(pwr + 16 * s2);

@@ -56,7 +56,7 @@ struct StepArgs {
   float* stage_k;               // [rows][bs][Hk][D] or null
   float* stage_v;
   int64_t* owner;               // [rows][bs]
-  _Float16* kimg;               // [rows][bs / 32][Hk][kImgHalfs] or null
+  _Float16* kimg;               // [rows][bs / 32][Hk][kKImgHalfs] or null
   _Float16* vimg;
   int32_t stage_rows;           // 0: no window
   float* q_rot;                 // [N][Hq][D]
@@ -268,12 +268,19 @@ __device__ void write_vector(const WriteCtx& a, const floatx4& y, int t, int h, 
   float* dst = a.stage + (seat * a.num_kv_heads + h) * kHeadDim;
   *reinterpret_cast<floatx4*>(dst + 4 * lane) = y;
   if (a.img != nullptr) {
-    _Float16* img = a.img + image_of(arow, (int)prow, a.block_size, h, a.num_kv_heads) * kImgHalfs;
+    const int64_t tile = image_of(arow, (int)prow, a.block_size, h, a.num_kv_heads);
     const int tt = (int)(prow & 31);
+    if (side == 0) {
+      _Float16* img = a.img + tile * kKImgHalfs;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int f = 4 * lane + c;
-      img[side == 0 ? kimg_offset(f, tt) : vimg_offset(f, tt)] = (_Float16)y[c];
+      for (int c = 0; c < 4; ++c) {
+        _Float16* d = img + kimg_offset(4 * lane + c, tt);
+        k_parts(y[c], d[0], d[kImgHalfs]);
+      }
+    } else {
+      _Float16* img = a.img + tile * kImgHalfs;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) img[vimg_offset(4 * lane + c, tt)] = (_Float16)y[c];
     }
   }
 }

@@ -1,7 +1,9 @@
 // fp16 operand images of the FP32 window arena (written by the window-write
 // kernels, read by the paged decode), per (arena row, 32-token tile, kv head):
-//   K image [16 k-steps m][64 lanes][8 slots]: lane t + 32g, slot 2i + b of
-//     step m = 2j + a holds feature 128g + 16j + 4a + i + 8b of token t;
+//   K image [2 parts][16 k-steps m][64 lanes][8 slots]: lane t + 32g, slot
+//     2i + b of step m = 2j + a holds feature 128g + 16j + 4a + i + 8b of
+//     token t; part 0 is RNE fp16(k), part 1 RNE fp16(k - part 0), so that
+//     the two parts carry k to about 2^-22 of its magnitude;
 //   V image [4 q][2 b][2 s][64 lanes][8 slots]: lane m + 32gs holds feature
 //     64q + 4(m >> 1) + 2b + (m & 1); slot u holds token 16s + 8gs +
 //     {0, 2, 1, 3, 4, 6, 5, 7}[u].
@@ -14,7 +16,14 @@
 
 namespace oscar {
 
-constexpr int kImgHalfs = 16 * 64 * 8;
+constexpr int kImgHalfs = 16 * 64 * 8;     // one operand image (V image; one K part)
+constexpr int kKImgHalfs = 2 * kImgHalfs;  // K image: high part, then low part
+
+// The two fp16 parts of a K value.
+__device__ __forceinline__ void k_parts(float x, _Float16& hi, _Float16& lo) {
+  hi = (_Float16)x;
+  lo = (_Float16)(x - (float)hi);
+}
 
 // Offsets of feature f of token t (0..31 within its tile) in the two images.
 __device__ __forceinline__ int kimg_offset(int f, int t) {

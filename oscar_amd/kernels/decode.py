@@ -68,10 +68,7 @@ def _stage_operands(stage, bs: int, hk: int):
         kimg, vimg = stage[3], stage[4]
     else:
         kimg, vimg = staging.stage_images(stage[0], stage[1])
-    want = staging.image_shape(rows, bs, hk)
-    if tuple(kimg.shape) != want or tuple(vimg.shape) != want or kimg.dtype != torch.float16 \
-            or vimg.dtype != torch.float16 or not (kimg.is_contiguous() and vimg.is_contiguous()):
-        raise ValueError(f"staging operand images must be contiguous fp16 {want}")
+    staging.check_images(kimg, vimg, rows, bs, hk)
     return owner, kimg, vimg, rows
 
 

@@ -40,12 +40,32 @@ def _v_image_tokens() -> torch.Tensor:
 
 
 def image_shape(rows: int, bs: int, hk: int) -> tuple:
+    """Shape of the V operand image of an arena."""
     return (rows, bs // 32, hk, IMAGE_HALFS)
+
+
+def k_image_shape(rows: int, bs: int, hk: int) -> tuple:
+    """Shape of the K operand image: a high and a low fp16 part per tile."""
+    return (rows, bs // 32, hk, 2 * IMAGE_HALFS)
+
+
+def check_images(k_image, v_image, rows: int, bs: int, hk: int) -> None:
+    """Raise unless the operand images are absent together or are contiguous
+    fp16 tensors of the arena's K and V image shapes (the kernels index them
+    from the arena geometry alone)."""
+    if k_image is None and v_image is None:
+        return
+    kwant, vwant = k_image_shape(rows, bs, hk), image_shape(rows, bs, hk)
+    if k_image is None or v_image is None or tuple(k_image.shape) != kwant or tuple(v_image.shape) != vwant \
+            or k_image.dtype != torch.float16 or v_image.dtype != torch.float16 \
+            or not (k_image.is_contiguous() and v_image.is_contiguous()):
+        raise ValueError(f"staging operand images must be contiguous fp16 {kwant} (K) and {vwant} (V)")
 
 
 def stage_images(stage_k: torch.Tensor, stage_v: torch.Tensor):
     """fp16 operand images of a whole arena (the layout oscar_staging_write
-    maintains incrementally): K [rows][bs/32][Hk][m][lane = t + 32g][slot],
+    maintains incrementally): K [rows][bs/32][Hk][part][m][lane = t + 32g][slot]
+    with part 0 = RNE fp16(k) and part 1 = RNE fp16(k - part 0),
     V [rows][bs/32][Hk][q][b][s][lane = m + 32gs][slot] with feature
     64q + 4(m // 2) + 2b + m % 2."""
     rows, bs, hk, d = stage_k.shape
@@ -53,9 +73,14 @@ def stage_images(stage_k: torch.Tensor, stage_v: torch.Tensor):
         raise ValueError("operand images need D = 256 and a block size that is a multiple of 32")
     T = bs // 32
     dev = stage_k.device
-    x = stage_k.view(rows, T, 32, hk, d).to(torch.float16)[..., _k_image_order().to(dev)]
-    x = x.view(rows, T, 32, hk, 2, 16, 8).permute(0, 1, 3, 5, 4, 2, 6)      # [r, T, hk, m, g, t, u]
-    kimg = x.reshape(rows, T, hk, IMAGE_HALFS).contiguous()
+    xf = stage_k.view(rows, T, 32, hk, d).float()[..., _k_image_order().to(dev)]
+    hi = xf.to(torch.float16)
+    lo = (xf - hi.float()).to(torch.float16)
+    parts = []
+    for x in (hi, lo):
+        x = x.view(rows, T, 32, hk, 2, 16, 8).permute(0, 1, 3, 5, 4, 2, 6)  # [r, T, hk, m, g, t, u]
+        parts.append(x.reshape(rows, T, hk, IMAGE_HALFS))
+    kimg = torch.cat(parts, -1).contiguous()
     y = stage_v.view(rows, T, 32, hk, d).to(torch.float16).permute(0, 1, 3, 4, 2)  # [r, T, hk, f, tok]
     y = y[..., _v_image_tokens().to(dev)]                                    # [r, T, hk, f, (s, gs, u)]
     y = y.reshape(rows, T, hk, 4, 16, 2, 2, 2, 2, 8)                        # f = (q, bl, b, e)
@@ -77,6 +102,7 @@ def staging_write(key, value, slot_mapping, qsl_dev, seq_dev, num_requests: int,
     if kr.stride(1) != 1 or vr.stride(0) != kr.stride(0) or vr.stride(1) != 1:
         kr, vr = kr.contiguous(), vr.contiguous()
     slots = slot_mapping.to(torch.int64).contiguous()
+    check_images(k_image, v_image, owner.shape[0], block_size, num_kv_heads)
     _lib.call("oscar_staging_write", _lib.ptr(kr), _lib.ptr(vr), kr.stride(0), _lib.ptr(slots), N,
               _lib.ptr(qsl_dev), _lib.ptr(seq_dev), num_requests, num_kv_heads, head_size, block_size,
               owner.shape[0], sink_eff, recent, _lib.ptr(R_k), _lib.ptr(R_v), _lib.ptr(stage_k),

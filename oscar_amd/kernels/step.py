@@ -14,7 +14,7 @@ import ctypes
 import torch
 
 from ..format import check_d
-from . import _lib
+from . import _lib, staging
 from .quant import cache_geometry
 
 MAX_STEP_TOKENS = 1024
@@ -72,6 +72,7 @@ def step_write(query, key, value, R_k, R_v, slot_mapping, qsl, seqs, k_cache, v_
         rows = owner.shape[0]
         if owner.dtype != torch.int64 or owner.shape[1] != bs:
             raise ValueError("staging owner must be int64 [rows, block_size]")
+        staging.check_images(kimg, vimg, rows, bs, num_kv_heads)
     else:
         sk = sv = owner = kimg = vimg = None
         rows = 0

@@ -3,14 +3,14 @@
 500-586): INT2 middle, FP32 sink when fully staged and the staged run ending at
 the last position, merged by log-sum-exp.  The library instead runs one pass
 in which a staged value replaces the INT2 one only inside those segments.
-Tolerance (fp32 output, stated): max |gpu - oracle| <= 2e-3 * max |oracle|;
+Tolerance (fp32 output, stated): max |gpu - oracle| <= 1e-3 * max |oracle|;
 impl-level (bf16 output): |gpu - oracle| <= 2e-2 + 2^-8 |oracle| elementwise.
-The kernel takes q and staged keys as fp16 MFMA operands.  A short request
-whose whole history is sink + tail (every key staged) with a sharp softmax
-shows that rounding directly: 1.1e-3 of the output maximum on the
-random-byte case below, where rounding q, K, V and p to fp16 in an fp64 CPU
-computation of the same request reproduces the GPU output to 2.9e-4.  Long
-histories stay below 1e-3, as on the MTP route.
+The kernel takes q and staged keys as fp16 high + low operand pairs (both to
+about 2^-22); staged values and the probabilities are single fp16 operands,
+with the row sums taken over the same rounded weights.  What remains is the
+fp16 rounding of a staged value (at most 2^-11 of it), largest when one staged
+token dominates a short request: the worst of a 150-case random sweep of MTP
+and DecodeOnly reads is 0.56e-3 of the output maximum, on such requests.
 """
 from types import SimpleNamespace as NS
 
@@ -25,7 +25,7 @@ from tests.test_gpu_backend import run_steps, within_bf16
 
 pytestmark = pytest.mark.gpu
 
-REL_TOL = 2e-3
+REL_TOL = 1e-3
 D = 256
 
 

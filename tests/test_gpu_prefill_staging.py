@@ -33,9 +33,9 @@ def _gpu_arena(arena, device):
     winner = torch.full(arena.owner.shape, -1, dtype=torch.int32, device=device)
     kimg = vimg = None
     if arena.bs % 32 == 0:
-        shape = staging.image_shape(arena.rows, arena.bs, arena.stage_k.shape[2])
-        kimg = torch.zeros(shape, dtype=torch.float16, device=device)
-        vimg = torch.zeros(shape, dtype=torch.float16, device=device)
+        geom = (arena.rows, arena.bs, arena.stage_k.shape[2])
+        kimg = torch.zeros(staging.k_image_shape(*geom), dtype=torch.float16, device=device)
+        vimg = torch.zeros(staging.image_shape(*geom), dtype=torch.float16, device=device)
     return sk, sv, owner, winner, kimg, vimg
 
 

@@ -3,7 +3,7 @@
 Each case draws page size, kv heads / group, request count, history and
 query lengths (page edges included), window geometry, and cache dtype.  It
 runs the MTP decode (1e-3 of the output scale), the DecodeOnly read over
-the same caches (2e-3), the pre-rotated quantize-write (bit-exact, random
+the same caches (1e-3), the pre-rotated quantize-write (bit-exact, random
 caches, skipped and out-of-range slots, clip ratios), and the prefill
 continuation (bf16 contract 2e-2 + 2^-8 |oracle|).  The seeds are fixed, so
 the cases are the same on every run."""
@@ -59,7 +59,7 @@ def test_decode_routes_random_shapes(device, params):
     want = oatt.decode_only_ref(last, L.k_cache, L.v_cache, case.bt, case.seqs, L.scale, L.num_kv_heads, D, arena)
     got = decode.decode_only(last.to(device), kc, vc, bt, case.seqs, L.scale, dstage, L.sink, L.recent).cpu()
     assert torch.isfinite(got).all()
-    assert (got - want).abs().max() <= 2e-3 * max(want.abs().max().item(), 1e-6)
+    assert (got - want).abs().max() <= 1e-3 * max(want.abs().max().item(), 1e-6)
 
 
 def write_prefill_cases(seed, n):

@@ -292,7 +292,9 @@ def test_operand_image_layouts_follow_their_formulas():
     """The fp16 window images the decode reads as MFMA operands, element by element:
     K block m, lane t + 32g, slot u = feature 128g + 16(m // 2) + 4(m % 2) + u // 2 + 8(u % 2)
     of token t; V block (q, b, s), lane m + 32gs, slot u = feature 64q + 4(m // 2) + 2b + m % 2
-    of token 16s + 8gs + (0, 2, 1, 3, 4, 6, 5, 7)[u]."""
+    of token 16s + 8gs + (0, 2, 1, 3, 4, 6, 5, 7)[u].  The K image's second part holds
+    fp16(k - fp16(k)) in the same order, so that the two parts sum to k within 2^-22 |k| + 2^-25
+    (half the spacing of fp16 subnormals, where the low part of a small k lies)."""
     from oscar_amd.kernels import staging as kstaging
 
     g = torch.Generator().manual_seed(3)
@@ -301,14 +303,17 @@ def test_operand_image_layouts_follow_their_formulas():
     kimg, vimg = kstaging.stage_images(sk, sv)
     order = [0, 2, 1, 3, 4, 6, 5, 7]
     for r, tile in ((0, 0), (1, 1)):
-        K = kimg[r, tile, 0].view(16, 64, 8)
+        K, KL = kimg[r, tile, 0].view(2, 16, 64, 8)
         V = vimg[r, tile, 0].view(4, 2, 2, 64, 8)
         for lane in range(64):
             t, gg = lane % 32, lane // 32
             for m in range(16):
                 for u in range(8):
                     f = 128 * gg + 16 * (m // 2) + 4 * (m % 2) + u // 2 + 8 * (u % 2)
-                    assert K[m, lane, u] == sk[r, 32 * tile + t, 0, f].half()
+                    x = sk[r, 32 * tile + t, 0, f]
+                    assert K[m, lane, u] == x.half()
+                    assert KL[m, lane, u] == (x - x.half().float()).half()
+                    assert abs(K[m, lane, u].double() + KL[m, lane, u].double() - x.double()) <= 2.0 ** -22 * abs(x) + 2.0 ** -25
             mm, gs = lane % 32, lane // 32
             for q in range(4):
                 for b in range(2):
