@@ -80,6 +80,11 @@ def _is_decode_only(state) -> bool:
     return getattr(state, "name", None) == "DecodeOnly" or state == OscarAttentionState.DecodeOnly.value
 
 
+def _capturing(t: torch.Tensor) -> bool:
+    """True while t's device stream is being captured into a graph."""
+    return t.is_cuda and torch.cuda.is_current_stream_capturing()
+
+
 class OscarAttentionBackendImpl:
     """Mixed into the native FULL-attention impl class by the plugin."""
 
@@ -98,6 +103,7 @@ class OscarAttentionBackendImpl:
         self._oscar_cfg = cfg
         self._oscar_stage_ready = False
         self._oscar_stats = {"writes": 0, "kv_bytes_written": 0, "reads": 0}
+        self._oscar_fixed_step_capture = False
         if cfg.verbose:
             print(f"[oscar-amd] OSCAR impl active: D={self.head_size}, slot=160B (K 96B + V 64B), "
                   f"Hq={self.num_heads}, Hk={self.num_kv_heads}, clip={cfg.k_clip_ratio}/{cfg.v_clip_ratio}, "
@@ -106,6 +112,14 @@ class OscarAttentionBackendImpl:
     @property
     def _oscar(self) -> OscarConfig:
         return self._oscar_cfg
+
+    def allow_fixed_step_capture(self, allow: bool = True) -> None:
+        """Let forward run under HIP graph capture.  Its launch arguments are
+        built from the step's host-side request lengths (query_start_loc_cpu,
+        seq_lens), so a replay repeats the captured step exactly: valid only
+        when every replay is that same step (a benchmark), never for an
+        engine's decode graphs, whose replays carry new lengths."""
+        self._oscar_fixed_step_capture = bool(allow)
 
     # ------------------------------------------------------------------ caches / rotations
     def _set_caches(self, kv_cache) -> None:
@@ -240,6 +254,11 @@ class OscarAttentionBackendImpl:
         num_tokens = query.shape[0]
         if attn_metadata is None:
             return output.fill_(0)
+        if _capturing(query) and not getattr(self, "_oscar_fixed_step_capture", False):
+            # The reference plugin likewise runs eagerly (delivery/serve_oscar.sh:54-55).
+            raise RuntimeError("OSCAR attention cannot be captured into an engine's graphs: its launch arguments "
+                               "come from the step's host-side request lengths, which every replay would reuse; "
+                               "serve with --enforce-eager")
         self._set_caches(kv_cache)
         if key is None or value is None:
             # backend.py:304-309: without fresh K/V only the DecodeOnly state

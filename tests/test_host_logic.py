@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from oracle.staging import arena_geometry
-from oscar_amd import integration, plugin, rotation
+from oscar_amd import backend, integration, plugin, rotation
 from oscar_amd.backend import OscarAttentionBackendImpl, metadata_batch_lists
 from oscar_amd.config import OscarConfig
 
@@ -233,6 +233,21 @@ def test_forward_without_metadata_zeroes_output(clean_env):
     out = torch.full((3, 6, 256), 5.0)
     caches = [torch.zeros(2, 128, 1, 256, dtype=torch.int8) for _ in range(2)]
     assert torch.count_nonzero(impl.forward(NS(layer_name="l.0"), out, out, out, caches, None, output=out)) == 0
+
+
+def test_forward_refuses_engine_graph_capture(clean_env, monkeypatch):
+    """Launch arguments come from host-side lengths: under capture, forward
+    raises unless the caller declared that every replay repeats the step."""
+    impl = make_impl(clean_env)
+    out = torch.zeros(3, 6, 256)
+    caches = [torch.zeros(2, 128, 1, 256, dtype=torch.int8) for _ in range(2)]
+    md = NS(attn_state=None)
+    monkeypatch.setattr(backend, "_capturing", lambda t: True)
+    with pytest.raises(RuntimeError, match="enforce-eager"):
+        impl.forward(NS(layer_name="l.0"), out, out, out, caches, md, output=out)
+    impl.allow_fixed_step_capture()
+    with pytest.raises(NotImplementedError):       # past the check: key = None outside DecodeOnly
+        impl.forward(NS(layer_name="l.0"), out, None, None, caches, md, output=out)
 
 
 def test_forward_without_fresh_kv_needs_the_decode_only_state(clean_env):
