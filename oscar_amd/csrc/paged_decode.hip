@@ -1042,8 +1042,11 @@ __global__ __launch_bounds__(kRotThreads) void paged_decode_merge_rotate_kernel(
   __shared__ __attribute__((aligned(16))) float orow[kHeadDim];
   __shared__ float csum[kRotWaves][64];
   static_assert(kMaxPartials <= kRotThreads, "one partial per thread");
-  const int qd = blockIdx.x & 3;
-  const int r = blockIdx.x >> 2;
+  // blockIdx.x = (r & 7) + 8 qd + 32 (r >> 3): workgroups are dealt to the 8
+  // XCDs by linear id mod 8, so the four quarter blocks of row r, which all
+  // read the row's every partial, share one XCD and its L2.
+  const int qd = (blockIdx.x >> 3) & 3;
+  const int r = (blockIdx.x & 7) + 8 * (blockIdx.x >> 5);
   const int item = blockIdx.y;
   const int rt = blockIdx.z;
   const ItemInfo it = a.items[item];
@@ -1317,7 +1320,7 @@ int launch_merge(const DecodeArgs& a, int64_t max_rows, unsigned nitems, const O
                  hipStream_t stream) {
   const int mr = merge_rows(max_rows);
   if (orot.rot_t != nullptr) {
-    dim3 grid((unsigned)(mr * 4), nitems, (unsigned)a.row_tiles);
+    dim3 grid((unsigned)(32 * ((mr + 7) / 8)), nitems, (unsigned)a.row_tiles);
     hipLaunchKernelGGL(paged_decode_merge_rotate_kernel, grid, dim3(kRotThreads), 0, stream, a, orot.rot_t, orot.out,
                        orot.out_stride, (int)orot.out_bf16);
   } else if (a.max_splits + a.fresh <= kSmallP) {
