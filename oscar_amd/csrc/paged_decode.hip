@@ -541,15 +541,15 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
     const int pgw = pick4(pgs[0], pgs[1], pgs[2], pgs[3], w);
     const int p0 = tbase + kTile * w;
     const int nvalid = pgw >= 0 ? min(kTile, max(prefix - p0, 0)) : 0;
-    // A tile with window tokens reads the first half of their K operand
-    // image now, a phase before the score pass uses it (the second half goes
-    // out at the start of that pass).
+    // A tile with window tokens reads the high part of their K operand image
+    // now, a phase before the score pass uses it (the low part reuses these
+    // registers inside that pass).
     const u32x4* img = reinterpret_cast<const u32x4*>(
         a.kimg + image_index(a, wmw != 0u ? pgw : 0, (int)fast_mod((uint32_t)p0, a.bs_div), kvh) * kKImgHalfs);
     u32x4 im[16];
     if (wmw != 0u) {
 #pragma unroll
-      for (int m = 0; m < 8; ++m) im[m] = img[m * 64 + lane];
+      for (int m = 0; m < 16; ++m) im[m] = img[m * 64 + lane];
     }
 
     // ---- own tile: token parameters and byte-transposed V codes ----
@@ -621,8 +621,6 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
           qk_pair(j, ka[0], ka[1]);
         }
       } else {
-#pragma unroll
-        for (int m = 8; m < 16; ++m) im[m] = img[m * 64 + lane];
         const bool wl = (wmw >> col) & 1u;
         const u32x4* img_lo = img + 16 * 64;
 #pragma unroll
