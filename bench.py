@@ -280,8 +280,22 @@ def bench_forward(dev, states, steps, warmup):
         s = st.step
         return lambda: st.impl.forward(st.layer, s.q, s.k, s.v, st.caches, s.md, output=out)
 
-    us = graph_us([call(st, o) for st, o in zip(states, outs)], steps, warmup)
-    return {"us": us, "out0": outs[0].clone()}
+    calls = [call(st, o) for st, o in zip(states, outs)]
+    us = graph_us(calls, steps, warmup)
+    out0 = outs[0].clone()
+    # The same forwards launched from Python one after another (no graph):
+    # the per-layer wall time an eager engine sees, host work included.
+    import time
+
+    for c in calls:
+        c()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        calls[i % len(calls)]()
+    torch.cuda.synchronize()
+    eager = (time.perf_counter() - t0) * 1e6 / steps
+    return {"us": us, "eager_us": eager, "out0": out0}
 
 
 def bench_quant_write(dev, steps=64):
@@ -614,7 +628,7 @@ def main():
     fwd = None
     if "forward" in parts:
         fwd = bench_forward(dev, states, args.steps, args.warmup)
-        log(f"bench: forward {fwd['us']:.3f} us/layer")
+        log(f"bench: forward {fwd['us']:.3f} us/layer (eager {fwd['eager_us']:.1f})")
     qw = None
     if "quant_write" in parts:
         qw = bench_quant_write(dev)
@@ -658,6 +672,9 @@ def main():
                             "INT2 write and window write of the 4 new tokens), decode, merge with R_v^T and the "
                             "bf16 cast; bf16 in and out",
                 "us_per_layer": round(fwd["us"], 3), "steps": args.steps, "warmup": args.warmup,
+                "eager_us_per_layer": round(fwd["eager_us"], 3),
+                "eager": "the same forwards launched one by one from Python without a graph, wall clock "
+                         "over the steps (host work included)",
                 "parity_max_abs_err_vs_oracle": fwd_err},
             "quant_write": None if qw is None else {
                 "workload": "C5 write: 65536 tokens bf16, Hk=1, random slots ~1/16 skipped, rotation on MFMA, "

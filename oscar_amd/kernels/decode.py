@@ -38,6 +38,38 @@ def validate_layout(qsl, seqs):
     return lengths
 
 
+class RequestLayout:
+    """A step's request layout, validated once and shared by the launches of
+    every layer in the step: query lengths, the longest query and history,
+    and the host int32 arrays (query starts, sequence lengths) the library
+    copies into its kernel arguments."""
+
+    __slots__ = ("qsl", "seqs", "lengths", "max_q", "max_hist", "qstart", "seq_t")
+
+    def __init__(self, qsl, seqs):
+        self.qsl = tuple(int(x) for x in qsl)
+        self.seqs = tuple(int(x) for x in seqs)
+        self.lengths = validate_layout(self.qsl, self.seqs)
+        self.max_q = max(self.lengths, default=0)
+        self.max_hist = max((s - m for s, m in zip(self.seqs, self.lengths)), default=0)
+        self.qstart = (ctypes.c_int32 * max(len(self.qsl), 1))(*self.qsl)
+        self.seq_t = (ctypes.c_int32 * max(len(self.seqs), 1))(*self.seqs)
+
+
+_LAST_LAYOUT: list = [None]
+
+
+def request_layout(qsl, seqs) -> RequestLayout:
+    """The RequestLayout of (qsl, seqs), reused while consecutive calls (the
+    layers of one step) pass the same lengths."""
+    key = (tuple(qsl), tuple(seqs))
+    hit = _LAST_LAYOUT[0]
+    if hit is None or hit[0] != key:
+        hit = (key, RequestLayout(*key))
+        _LAST_LAYOUT[0] = hit
+    return hit[1]
+
+
 class DecodePlan:
     """Device-resident arguments of one decode launch; ``launch`` only enqueues.
 
@@ -81,13 +113,12 @@ def plan(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None, out=None,
     n, hq, d = q.shape
     check_d(d)
     hk = k.shape[1]
-    lengths = validate_layout(qsl, seqs)
-    if sum(lengths) != n:
+    lay = request_layout(qsl, seqs)
+    if sum(lay.lengths) != n:
         raise ValueError("Query layout does not match actual query tokens")
-    max_q = max(lengths) if lengths else 0
+    max_q, max_hist = lay.max_q, lay.max_hist
     if max_q > MAX_QUERY_LEN:
         raise ValueError(f"paged decode supports at most {MAX_QUERY_LEN} query tokens per request")
-    max_hist = max((s - m for s, m in zip(seqs, lengths)), default=0)
     dev = q.device
     q = q.float().contiguous()
     k = k.float().contiguous()
@@ -97,15 +128,14 @@ def plan(q, k, v, kc, vc, bt, qsl, seqs, scale: float, stage=None, out=None,
     bt = bt.to(device=dev, dtype=torch.int32).contiguous()
     # Request layout as host int32 arrays: the library copies it into the
     # kernel arguments (no device metadata round trip).
-    qstart = (ctypes.c_int32 * len(qsl))(*[int(x) for x in qsl])
-    seq_t = (ctypes.c_int32 * max(len(seqs), 1))(*[int(x) for x in seqs])
+    qstart, seq_t = lay.qstart, lay.seq_t
     bs, pages, kst, vst = cache_geometry(kc, vc)
     if stage is not None:
         owner, kimg, vimg, rows = _stage_operands(stage, bs, hk)
     else:
         owner = kimg = vimg = None
         rows = 0
-    B = len(lengths)
+    B = len(lay.lengths)
     if bs % 32:
         raise ValueError("paged decode needs a cache block size that is a multiple of 32")
     need = _lib.load().oscar_paged_decode_workspace_bytes(B, hk, hq, max(max_q, 1), max_hist, tiles_per_split)

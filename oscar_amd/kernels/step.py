@@ -14,7 +14,7 @@ import ctypes
 import torch
 
 from ..format import check_d
-from . import _lib, staging
+from . import _lib, decode, staging
 from .quant import cache_geometry
 
 MAX_STEP_TOKENS = 1024
@@ -62,8 +62,8 @@ def step_write(query, key, value, R_k, R_v, slot_mapping, qsl, seqs, k_cache, v_
     B = len(qsl) - 1
     if len(seqs) < B:
         raise ValueError("one sequence length per request")
-    qstart = (ctypes.c_int32 * max(len(qsl), 1))(*[int(x) for x in qsl])
-    seq_t = (ctypes.c_int32 * max(B, 1))(*[int(x) for x in seqs[:B]])
+    lay = decode.request_layout(qsl, seqs[:B])
+    qstart, seq_t = lay.qstart, lay.seq_t
     bs, pages, kst, vst = cache_geometry(k_cache, v_cache)
     if stage is not None:
         sk, sv, owner = stage[0], stage[1], stage[2]

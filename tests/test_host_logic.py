@@ -337,3 +337,17 @@ def test_operand_image_layouts_follow_their_formulas():
                             f = 64 * q + 4 * (mm // 2) + 2 * b + mm % 2
                             tok = 16 * s + 8 * gs + order[u]
                             assert V[q, b, s, lane, u] == sv[r, 32 * tile + tok, 0, f].half()
+
+
+def test_request_layout_is_built_once_per_step():
+    """The layers of a step share one validated layout; new lengths build a new one."""
+    from oscar_amd.kernels import decode as kdecode
+
+    a = kdecode.request_layout([0, 4, 5], [100, 7])
+    assert kdecode.request_layout((0, 4, 5), (100, 7)) is a
+    assert a.lengths == [4, 1] and a.max_q == 4 and a.max_hist == 96
+    assert list(a.qstart) == [0, 4, 5] and list(a.seq_t) == [100, 7]
+    b = kdecode.request_layout([0, 4, 5], [101, 7])
+    assert b is not a and b.max_hist == 97
+    with pytest.raises(ValueError):
+        kdecode.request_layout([0, 4, 5], [3, 7])         # history would be negative
