@@ -34,7 +34,8 @@ struct CacheArgs {
   int64_t k_page, k_tok, k_head;     // byte strides
   int64_t v_page, v_tok, v_head;
   int32_t block_size;
-  int64_t num_slots;                 // pages * block_size; larger slots are skipped
+  int64_t num_slots;                 // pages * block_size (< 2^31); larger slots are skipped
+  FastDiv bs_div;                    // block_size
 };
 
 // Exact value of ascending-sorted |x| at index `idx` over the 256 values held
@@ -214,7 +215,7 @@ __device__ void quantize_store(const float (&v)[kPerLane], const QParams& p, int
     words[w] = acc;
   }
   if (slot < 0 || slot >= c.num_slots) return;
-  const int64_t page = slot / c.block_size;
+  const int64_t page = fast_div((uint32_t)slot, c.bs_div);
   const int64_t row = slot - page * c.block_size;
   uint8_t* kslot = c.k_cache + page * c.k_page + row * c.k_tok + (int64_t)head * c.k_head;
   uint8_t* dst;
@@ -433,13 +434,15 @@ __global__ void rotation_operand_kernel(const float* __restrict__ R, __bf16* __r
   out[idx] = p == 0 ? hi : (__bf16)(x - (float)hi);
 }
 
-int check_cache_args(const CacheArgs& c) {
+int check_cache_args(CacheArgs& c) {
   if (c.block_size <= 0 || c.num_slots <= 0 || c.k_cache == nullptr || c.v_cache == nullptr)
     return kErrInvalidArgument;
+  if (c.num_slots >= ((int64_t)1 << 31)) return kErrUnsupportedGeometry;
   if (c.k_head < kKCodeOff + kCodeBytes || c.v_head < kCodeBytes) return kErrUnsupportedGeometry;
   const int64_t strides[6] = {c.k_page, c.k_tok, c.k_head, c.v_page, c.v_tok, c.v_head};
   for (int64_t s : strides)
     if (s <= 0 || (s & 15) != 0) return kErrUnsupportedGeometry;
+  c.bs_div = make_fast_div((uint32_t)c.block_size);
   if ((reinterpret_cast<uintptr_t>(c.k_cache) & 15) || (reinterpret_cast<uintptr_t>(c.v_cache) & 15))
     return kErrUnsupportedGeometry;
   return kOk;
@@ -485,7 +488,7 @@ int oscar_quant_write_prerotated(const float* k_rot, const float* v_rot, int64_t
     return kErrInvalidArgument;
   CacheArgs c{static_cast<uint8_t*>(k_cache), static_cast<uint8_t*>(v_cache), k_stride_page,
               k_stride_token, k_stride_head, v_stride_page, v_stride_token, v_stride_head,
-              block_size, num_pages * (int64_t)block_size};
+              block_size, num_pages * (int64_t)block_size, FastDiv{}};
   int st = check_cache_args(c);
   if (st != kOk) return st;
   dim3 grid((unsigned)((num_tokens + 127) / 128), (unsigned)(num_kv_heads * 2));
@@ -517,7 +520,7 @@ int oscar_quant_write(const void* key_bf16, const void* value_bf16, int64_t num_
     return kErrInvalidArgument;
   CacheArgs c{static_cast<uint8_t*>(k_cache), static_cast<uint8_t*>(v_cache), k_stride_page,
               k_stride_token, k_stride_head, v_stride_page, v_stride_token, v_stride_head,
-              block_size, num_pages * (int64_t)block_size};
+              block_size, num_pages * (int64_t)block_size, FastDiv{}};
   int st = check_cache_args(c);
   if (st != kOk) return st;
   if (set_dynamic_lds(reinterpret_cast<const void*>(quant_write_fused_kernel), (int)kFusedLds, g_lds_set) != kOk) return kErrLaunch;
