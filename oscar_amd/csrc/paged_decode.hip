@@ -116,6 +116,7 @@ struct DecodeArgs {
   float* ws;                    // partials
   const int32_t* win;           // DecodeOnly: (head, cut) per chunk request; null: every position
   int32_t fresh;                // 1: the fresh-token partial exists (MTP read); 0: DecodeOnly
+  int32_t fresh_block;          // 1: a workgroup of its own computes it (x = max_splits); 0: a history split does
   int32_t max_splits, row_tiles;
   ItemInfo items[kMaxInlineItems];
 };
@@ -285,8 +286,7 @@ __device__ __forceinline__ int64_t image_index(const DecodeArgs& a, int page, in
 }
 // The step's own new tokens of one item, exact fp32: row (token j, head h)
 // against new keys 0 .. j, written as a partial like a history split's.
-__device__ void fresh_partial(const DecodeArgs& a, const ItemInfo& it, int item, int rt, FreshLds& F) {
-  const int tid = threadIdx.x;
+__device__ void fresh_partial(const DecodeArgs& a, const ItemInfo& it, int item, int rt, FreshLds& F, int tid) {
   const int nq = it.nq, kvh = it.kvh;
   const int rows = nq * a.group;
   const int r = tid >> 3, c = tid & 7;
@@ -392,19 +392,29 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   // longest workgroups, so they start first (measured: C5 decode 37.6 ->
   // 34 us, C2 unchanged).
   const int bx = blockIdx.x;
-  const int split = bx >= a.max_splits ? bx : (bx == 0 ? 0 : a.max_splits - bx);
   const int item = blockIdx.y;
   const int rt = blockIdx.z;
   const ItemInfo it = a.items[item];
   const int rows = it.nq * a.group;
   if (it.nq <= 0 || rt * kRows >= rows) return;
-  if (split == a.max_splits) {
-    if (a.fresh) fresh_partial(a, it, item, rt, *reinterpret_cast<FreshLds*>(smem_raw));
+  if (a.fresh_block && bx == a.max_splits) {
+    fresh_partial(a, it, item, rt, *reinterpret_cast<FreshLds*>(smem_raw), (int)threadIdx.x);
     return;
   }
+  const int split = bx == 0 ? 0 : a.max_splits - bx;
   const int prefix = it.prefix;
   const int steps = (prefix + kStepTok - 1) / kStepTok;
-  if (split >= steps) return;
+  // Without a workgroup of its own (when one more per item would not find a
+  // resident slot), the step's own new tokens (the fresh partial, partial
+  // slot S) go to an idle split when the history has fewer steps than there
+  // are splits, else to the middle split, whose steps hold no window tokens
+  // (sink and recent tokens lie in the first and last steps).
+  const int fresh_split = steps < a.max_splits ? steps : a.max_splits / 2;
+  const bool fresh_here = a.fresh && !a.fresh_block && split == fresh_split;
+  if (split >= steps) {
+    if (fresh_here) fresh_partial(a, it, item, rt, *reinterpret_cast<FreshLds*>(smem_raw), (int)threadIdx.x);
+    return;
+  }
   MainLds& S = *reinterpret_cast<MainLds*>(smem_raw);
 
   const int tid = threadIdx.x;
@@ -844,6 +854,13 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
     part[kPartO + lane] = m_run;
     part[kPartO + kRows + lane] = lt;
   }
+  if (fresh_here) {
+    __syncthreads();               // the history's LDS is no longer read
+    // the thread index rebuilt from the wave index and the lane count, so
+    // that no register holds it through the steps
+    const int ftid = 64 * w + (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    fresh_partial(a, it, item, rt, *reinterpret_cast<FreshLds*>(smem_raw), ftid);
+  }
 }
 
 // One 256-thread block per (output row, quarter of the features) of an item.
@@ -1216,16 +1233,26 @@ int64_t splits_for(int64_t max_history, int tiles_per_split) {
   return (tiles + tiles_per_split - 1) / tiles_per_split;
 }
 
+int32_t requests_per_launch(int32_t num_kv_heads);
+
+// Split workgroups resident at once: two per CU on MI355X's 256 CUs.
+constexpr int64_t kResidentSplitWgs = 512;
+
 int default_tiles_per_split(int32_t num_requests, int32_t num_kv_heads, int64_t max_history) {
-  // Enough workgroups to cover the GPU for one long request (two per CU),
-  // few enough that each runs several steps and the partials stay a fraction
-  // of the INT2 bytes read, and never more splits than the merge takes.
+  // As many splits per item as fill the GPU once (the fresh partial rides on
+  // a history workgroup, so no workgroup waits for a second round), never
+  // more than the history has steps or the merge takes.
   const int64_t tiles = max_history > 0 ? (max_history + kTile - 1) / kTile : 0;
-  const int64_t work = tiles * num_requests * num_kv_heads;
-  int tps = 4;
-  while (tps < 64 && work / tps > 512) tps *= 2;
-  while (tps < kMaxTilesPerSplit && (tiles + tps - 1) / tps > kMaxSplits) tps *= 2;
-  return tps;
+  if (tiles == 0) return kWaves;
+  const int64_t steps = (tiles + kWaves - 1) / kWaves;
+  const int32_t per = requests_per_launch(num_kv_heads);
+  const int64_t items = (int64_t)(num_requests < per ? num_requests : per) * num_kv_heads;
+  int64_t s = items > 0 ? kResidentSplitWgs / items : 1;
+  s = s < 1 ? 1 : s;
+  s = s < steps ? s : steps;
+  s = s < kMaxSplits ? s : kMaxSplits;
+  const int64_t tps = (tiles + s - 1) / s;
+  return (int)(tps < kWaves ? kWaves : (tps > kMaxTilesPerSplit ? kMaxTilesPerSplit : tps));
 }
 
 int32_t requests_per_launch(int32_t num_kv_heads) {
@@ -1417,7 +1444,11 @@ int paged_decode(const float* q_rot, const float* k_new, const float* v_new, int
     }
     a.block_table = block_table ? block_table + (int64_t)c0 * block_table_stride : nullptr;
     const unsigned nitems = (unsigned)(nreq * num_kv_heads);
-    dim3 grid((unsigned)(a.max_splits + 1), nitems, (unsigned)a.row_tiles);
+    // The fresh partial gets a workgroup of its own when one more per item
+    // still fits the resident budget, else it rides on a history split.
+    a.fresh_block = (int64_t)(a.max_splits + 1) * nitems <= kResidentSplitWgs ? 1 : 0;
+    const int gx = a.max_splits + a.fresh_block;
+    dim3 grid((unsigned)(gx > 0 ? gx : 1), nitems, (unsigned)a.row_tiles);
     hipLaunchKernelGGL(paged_decode_split_kernel, grid, dim3(256), kLdsBytes, stream, a);
     if (hipGetLastError() != hipSuccess) return kErrLaunch;
     if ((rc = launch_merge(a, (int64_t)max_query_len * a.group, nitems, orot, stream)) != kOk) return rc;

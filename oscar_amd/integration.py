@@ -59,16 +59,21 @@ DECODE_MAX_SPLITS = 1023               # history splits per item (the fresh-toke
 DECODE_MAX_TILES_PER_SPLIT = 256
 
 
+DECODE_RESIDENT_SPLITS = 512          # split workgroups resident at once (two per CU, 256 CUs)
+
+
 def decode_tiles_per_split(max_requests: int, num_kv_heads: int, max_history: int) -> int:
-    """The library's default split length (in tiles) for this batch shape."""
+    """The library's default split length (in tiles) for this batch shape:
+    as many splits per item as fill the GPU once, at most one per 4-tile
+    step and at most DECODE_MAX_SPLITS."""
     tiles = -(-max_history // DECODE_TILE) if max_history > 0 else 0
-    work = tiles * max_requests * num_kv_heads
-    tps = 4
-    while tps < 64 and work // tps > 512:
-        tps *= 2
-    while tps < DECODE_MAX_TILES_PER_SPLIT and -(-tiles // tps) > DECODE_MAX_SPLITS:
-        tps *= 2
-    return tps
+    if tiles == 0:
+        return 4
+    steps = -(-tiles // 4)
+    items = min(max_requests, DECODE_LAUNCH_ITEMS // num_kv_heads) * num_kv_heads
+    s = max(DECODE_RESIDENT_SPLITS // items, 1) if items > 0 else 1
+    s = min(s, steps, DECODE_MAX_SPLITS)
+    return min(max(-(-tiles // s), 4), DECODE_MAX_TILES_PER_SPLIT)
 
 
 def decode_workspace_bytes(max_requests: int, num_kv_heads: int, num_heads: int, max_query_len: int,
