@@ -406,10 +406,13 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   const int steps = (prefix + kStepTok - 1) / kStepTok;
   // Without a workgroup of its own (when one more per item would not find a
   // resident slot), the step's own new tokens (the fresh partial, partial
-  // slot S) go to an idle split when the history has fewer steps than there
-  // are splits, else to the middle split, whose steps hold no window tokens
-  // (sink and recent tokens lie in the first and last steps).
-  const int fresh_split = steps < a.max_splits ? steps : a.max_splits / 2;
+  // slot S) go to a split with the least history work that holds no window
+  // step (sink and recent tokens lie in the first and last steps): an idle
+  // split when the history has fewer steps than there are splits; else the
+  // last split when the steps do not divide evenly (it has one step fewer
+  // than the splits that hold the last steps); else the middle one.
+  const int rem = a.max_splits > 0 ? steps % a.max_splits : 0;
+  const int fresh_split = steps < a.max_splits ? steps : (rem != 0 ? a.max_splits - 1 : a.max_splits / 2);
   const bool fresh_here = a.fresh && !a.fresh_block && split == fresh_split;
   if (split >= steps) {
     if (fresh_here) fresh_partial(a, it, item, rt, *reinterpret_cast<FreshLds*>(smem_raw), (int)threadIdx.x);
