@@ -97,9 +97,9 @@ int oscar_quant_write_prerotated(const float* k_rot, const float* v_rot, int64_t
  *     history positions 0 .. seq_lens[i] - n_i - 1;
  *   max_query_len / max_history: host upper bounds used to size the grid;
  *   stage_owner [stage_rows][block_size] int64 and the window's fp16 operand
- *     images stage_k_image / stage_v_image [stage_rows][block_size / 32][Hk]
- *     [8192] (16-byte aligned, written by oscar_staging_write; stage_rows =
- *     0: no window);
+ *     images stage_k_image [stage_rows][block_size / 32][Hk][16384] /
+ *     stage_v_image [stage_rows][block_size / 32][Hk][8192] (16-byte
+ *     aligned, written by oscar_staging_write; stage_rows = 0: no window);
  *   tiles_per_split: 32-token tiles per split workgroup (0: automatic, at most 256);
  *   out [num_tokens][Hq][D] fp32 (rotated-V domain);
  *   workspace: >= oscar_paged_decode_workspace_bytes(...) bytes (same
@@ -253,6 +253,75 @@ int oscar_step_write(const void* query_bf16, int64_t query_token_stride, const v
                      void* stage_k_image, void* stage_v_image, int32_t stage_rows, int32_t sink_eff,
                      int32_t recent, float* q_rot, float* k_rot, float* v_rot, oscar_stream_t stream);
 
+/* ---------------------------------------------------------------- MTP forward
+ * The whole forward of one layer for a short step (every request has
+ * 1 .. 16 query tokens, at most 1024 tokens in all): oscar_step_write, then
+ * oscar_paged_decode_rotated over its q_rot / k_rot / v_rot, on one stream.
+ * Replaces the short-step route of the reference's forward
+ * (oscar_ascend/backend.py:239-319: the writes at 150-189 and 439-481, the
+ * paged read at 273-303 with the rotations and @ R_v^T at 291-295).
+ * Arguments and bytes written are those of the two entries; they come in
+ * two parts that a caller builds once and reuses:
+ *   oscar_mtp_layer: the layer's rotations, caches and window arena (fixed
+ *     while the layer lives; stage_rows = 0: no window, the arena pointers
+ *     are then ignored);
+ *   oscar_mtp_step: the step's request layout (host arrays), slot mapping,
+ *     block table and scratch, shared by every layer of the step; q_rot /
+ *     k_rot / v_rot are fp32 scratch of num_tokens x num_heads (num_kv_heads)
+ *     x D floats, workspace >= oscar_paged_decode_workspace_bytes(num_requests,
+ *     num_kv_heads, num_heads, max_query_len, max_history, tiles_per_split).
+ * Only the activations and the output pass per call: query_bf16
+ * [num_tokens][query_token_stride], key_bf16 / value_bf16
+ * [num_tokens][kv_token_stride], out [num_tokens][out_token_stride] bf16
+ * (out_bf16 = 1) or fp32 in the model domain.  The layer and the step must
+ * agree on num_heads and num_kv_heads.  Every argument is checked before
+ * anything is enqueued.
+ */
+typedef struct oscar_mtp_layer {
+  const float* rot_k;            /* [D][D] fp32, x_rot = x @ R_k */
+  const float* rot_v;            /* [D][D] fp32 */
+  const float* rot_v_t;          /* R_v^T [D][D] fp32, applied to the output */
+  void* k_cache;
+  void* v_cache;
+  int64_t num_pages;
+  int64_t k_stride_page, k_stride_token, k_stride_head;   /* bytes */
+  int64_t v_stride_page, v_stride_token, v_stride_head;   /* bytes */
+  int32_t block_size;
+  int32_t num_heads, num_kv_heads, head_size;
+  int32_t clip_index_k, clip_index_v;
+  float scale;
+  int32_t stage_rows;
+  float* stage_k;
+  float* stage_v;
+  int64_t* stage_owner;
+  void* stage_k_image;
+  void* stage_v_image;
+  int32_t sink_eff, recent;
+} oscar_mtp_layer;
+
+typedef struct oscar_mtp_step {
+  int32_t num_tokens, num_requests, max_query_len;
+  int64_t max_history;
+  const int32_t* query_start_loc;  /* HOST [num_requests + 1] */
+  const int32_t* seq_lens;         /* HOST [num_requests] */
+  const int64_t* slot_mapping;     /* [num_tokens] */
+  const int32_t* block_table;      /* [num_requests][block_table_stride] */
+  int64_t block_table_stride;
+  int32_t block_table_cols;
+  int32_t num_heads, num_kv_heads;
+  int32_t tiles_per_split;         /* 0: automatic */
+  float* q_rot;
+  float* k_rot;
+  float* v_rot;
+  void* workspace;
+  size_t workspace_size;
+} oscar_mtp_step;
+
+int oscar_mtp_forward(const oscar_mtp_layer* layer, const oscar_mtp_step* step, const void* query_bf16,
+                      int64_t query_token_stride, const void* key_bf16, const void* value_bf16,
+                      int64_t kv_token_stride, void* out, int64_t out_token_stride, int32_t out_bf16,
+                      oscar_stream_t stream);
+
 /* ---------------------------------------------------------------- window write
  * Record the step's tokens in the FP32 sink/recent staging arena.
  * Replaces the torch body of _staging_write (oscar_ascend/backend.py:439-481)
@@ -265,9 +334,10 @@ int oscar_step_write(const void* query_bf16, int64_t query_token_stride, const v
  * unclipped).  key/value: bf16 [num_tokens][token_stride]; rot_*: fp32 [D][D];
  * seat_winner: int32 [stage_rows][block_size] scratch that must hold -1 on
  * entry and is left at -1.  stage_k_image / stage_v_image (both or neither,
- * block_size % 32 == 0): fp16 [stage_rows][block_size / 32][Hk][8192]; a
- * kept winner also writes its values there in the decode kernel's MFMA
- * operand order.
+ * block_size % 32 == 0): fp16 [stage_rows][block_size / 32][Hk][16384] (K:
+ * the fp16 rounding of each value, then the fp16 rounding of what it left)
+ * and [stage_rows][block_size / 32][Hk][8192] (V); a kept winner also
+ * writes its values there in the decode kernel's MFMA operand order.
  */
 int oscar_staging_write(const void* key_bf16, const void* value_bf16, int64_t token_stride,
                         const int64_t* slot_mapping, int32_t num_tokens,

@@ -254,7 +254,8 @@ class OscarAttentionBackendImpl:
         num_tokens = query.shape[0]
         if attn_metadata is None:
             return output.fill_(0)
-        if _capturing(query) and not getattr(self, "_oscar_fixed_step_capture", False):
+        capturing = _capturing(query)
+        if capturing and not getattr(self, "_oscar_fixed_step_capture", False):
             # The reference plugin likewise runs eagerly (delivery/serve_oscar.sh:54-55).
             raise RuntimeError("OSCAR attention cannot be captured into an engine's graphs: its launch arguments "
                                "come from the step's host-side request lengths, which every replay would reuse; "
@@ -270,7 +271,7 @@ class OscarAttentionBackendImpl:
             output[:num_tokens] = attn_out.reshape(output[:num_tokens].shape).to(output.dtype)
             return output
 
-        if self._short_step(layer, query, key, value, kv_cache, attn_metadata, output):
+        if self._short_step(layer, query, key, value, kv_cache, attn_metadata, output, capturing):
             self._oscar_stats["reads"] += 1
             return output
         self.do_kv_cache_update(layer, key, value, kv_cache,
@@ -287,47 +288,60 @@ class OscarAttentionBackendImpl:
             output[:num_tokens] = attn_out.reshape(num_tokens, -1).to(output.dtype)
         return output
 
-    def _short_step(self, layer, query, key, value, kv_cache, attn_metadata, output) -> bool:
+    def _short_step(self, layer, query, key, value, kv_cache, attn_metadata, output, capturing: bool) -> bool:
         """The whole forward of a step whose requests all take the paged read
-        (0 < q_len <= 16, backend.py:273-303) in two library calls: the fused
+        (0 < q_len <= 16, backend.py:273-303) in one library call: the fused
         step write (q/k/v rotation, INT2 write, window write) and the decode
-        with R_v^T and the cast to the output dtype in its merge.  Returns
-        False (nothing done) when the step does not qualify."""
+        with R_v^T and the cast to the output dtype in its merge.  The layer's
+        arguments are packed once per layer and the step's once per step.
+        Returns False (nothing done) when the step does not qualify."""
         cfg = self._oscar
         N = attn_metadata.num_actual_tokens
-        if not cfg.use_paged or N <= 0 or N > step.MAX_STEP_TOKENS or query.shape[0] < N:
+        if not cfg.use_paged or N <= 0 or N > step.MAX_STEP_TOKENS or query.shape[0] < N or output.shape[0] < N:
             return False
         if output.dtype not in (torch.bfloat16, torch.float32) or query.dtype != torch.bfloat16 \
                 or key.dtype != torch.bfloat16 or value.dtype != torch.bfloat16:
             return False
+        if self.key_cache.shape[1] % 32:
+            return False
         qsl, seqs = metadata_batch_lists(attn_metadata)
-        if qsl[0] != 0 or qsl[-1] != N or any(b - a < 0 or b - a > cfg.paged_max_q_len
-                                              for a, b in itertools.pairwise(qsl)):
-            return False
-        bs = self.key_cache.shape[1]
-        if bs % 32:
-            return False
         dev = query.device
-        rk, rv = self._layer_rots(layer, dev)
-        stage = None
-        sink_eff = 0
-        if cfg.window_enabled:
-            self._ensure_staging(layer, kv_cache)
-            stage = (layer._oscar_stage_k, layer._oscar_stage_v, layer._oscar_slot_owner,
-                     layer._oscar_stage_kimg, layer._oscar_stage_vimg)
-            sink_eff = (cfg.sink_tokens // bs) * bs
-        D, Hq, Hk = self.head_size, self.num_heads, self.num_kv_heads
-        q_rot, k_rot, v_rot = step.step_write(
-            query, key, value, rk, rv, attn_metadata.slot_mapping[:N], qsl, seqs, self.key_cache,
-            self.value_cache, quant.clip_index(cfg.k_clip_ratio, D), quant.clip_index(cfg.v_clip_ratio, D),
-            Hq, Hk, stage, sink_eff, cfg.recent_tokens)
+        stream = _lib.stream_handle(dev)
+        st = step.mtp_step(qsl, seqs, N, attn_metadata.slot_mapping, attn_metadata.block_tables, self.num_heads,
+                           self.num_kv_heads, self.head_size, cfg.paged_max_q_len, dev, stream, reuse=not capturing)
+        if st is None:
+            return False
+        step.mtp_forward(self._mtp_layer(layer, kv_cache, dev), st, query, key, value, output, stream)
         self._oscar_stats["writes"] += 1
-        self._oscar_stats["kv_bytes_written"] += N * Hk * 160
-        decode.paged_attention(q_rot, k_rot, v_rot, self.key_cache, self.value_cache, attn_metadata.block_tables,
-                               qsl, seqs, self.scale, stage, out_rotation=layer._oscar_rvT, out=output[:N])
+        self._oscar_stats["kv_bytes_written"] += N * self.num_kv_heads * 160
         if output.shape[0] > N:
             output[N:].zero_()
         return True
+
+    def _mtp_layer(self, layer, kv_cache, dev) -> step.MtpLayer:
+        """The layer half of the short-step forward, kept on the layer and
+        rebuilt only when its rotations, caches or window arena are replaced."""
+        cfg = self._oscar
+        if cfg.window_enabled:
+            self._ensure_staging(layer, kv_cache)
+        rots = getattr(layer, "_oscar_rots", None)
+        if not rots:
+            rots = self._layer_rots(layer, dev)
+        arena = (layer._oscar_stage_k, layer._oscar_stage_v, layer._oscar_slot_owner, layer._oscar_stage_kimg,
+                 layer._oscar_stage_vimg) if cfg.window_enabled else (None,) * 5
+        ml = getattr(layer, "_oscar_mtp", None)
+        rvT = getattr(layer, "_oscar_rvT", None)
+        if ml is not None and ml.bound_to(rots[0], rots[1], rvT, self.key_cache, self.value_cache, *arena):
+            return ml
+        rk, rv = self._layer_rots(layer, dev)
+        D = self.head_size
+        bs = self.key_cache.shape[1]
+        ml = step.MtpLayer(rk, rv, layer._oscar_rvT, self.key_cache, self.value_cache, self.num_heads,
+                           self.num_kv_heads, quant.clip_index(cfg.k_clip_ratio, D),
+                           quant.clip_index(cfg.v_clip_ratio, D), self.scale,
+                           arena if cfg.window_enabled else None, (cfg.sink_tokens // bs) * bs, cfg.recent_tokens)
+        layer._oscar_mtp = ml
+        return ml
 
     def _decode_attention(self, layer, query, attn_metadata) -> torch.Tensor:
         """backend.py:321-358, 500-586 — one query token per request over its

@@ -60,6 +60,7 @@
 // [max(seq - recent, head), seq).
 #include "oscar_common.h"
 #include "window_images.h"
+#include "../../include/oscar_amd.h"
 
 namespace oscar {
 namespace {
@@ -1388,16 +1389,32 @@ size_t oscar_paged_decode_workspace_bytes(int32_t num_requests, int32_t num_kv_h
 namespace oscar {
 namespace {
 
-int paged_decode(const float* q_rot, const float* k_new, const float* v_new, int32_t num_tokens, int32_t num_heads,
-                 int32_t num_kv_heads, int32_t head_size, const void* k_cache, const void* v_cache,
-                 int32_t block_size, int64_t num_pages, int64_t k_stride_page, int64_t k_stride_token,
-                 int64_t k_stride_head, int64_t v_stride_page, int64_t v_stride_token, int64_t v_stride_head,
-                 const int32_t* block_table, int64_t block_table_stride, int32_t block_table_cols,
-                 const int32_t* query_start_loc, const int32_t* seq_lens, int32_t num_requests,
-                 int32_t max_query_len, int64_t max_history, const int64_t* stage_owner,
-                 const void* stage_k_image, const void* stage_v_image, int32_t stage_rows, float scale,
-                 int32_t tiles_per_split, float* out, const OutRotation& orot, void* workspace,
-                 size_t workspace_size, hipStream_t stream) {
+// A checked decode: the kernel arguments and the host request layout of one
+// oscar_paged_decode call, ready to enqueue (empty: nothing to launch).
+struct DecodeLaunch {
+  DecodeArgs a;
+  OutRotation orot;
+  const int32_t* qsl;
+  const int32_t* seqs;
+  const int32_t* block_table;
+  int64_t bt_stride;
+  int32_t num_requests;
+  int32_t max_query_len;
+  int32_t num_kv_heads;
+  bool empty;
+};
+
+int prepare_decode(DecodeLaunch& L, const float* q_rot, const float* k_new, const float* v_new, int32_t num_tokens,
+                   int32_t num_heads, int32_t num_kv_heads, int32_t head_size, const void* k_cache,
+                   const void* v_cache, int32_t block_size, int64_t num_pages, int64_t k_stride_page,
+                   int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page, int64_t v_stride_token,
+                   int64_t v_stride_head, const int32_t* block_table, int64_t block_table_stride,
+                   int32_t block_table_cols, const int32_t* query_start_loc, const int32_t* seq_lens,
+                   int32_t num_requests, int32_t max_query_len, int64_t max_history, const int64_t* stage_owner,
+                   const void* stage_k_image, const void* stage_v_image, int32_t stage_rows, float scale,
+                   int32_t tiles_per_split, float* out, const OutRotation& orot, void* workspace,
+                   size_t workspace_size) {
+  L.empty = true;
   if (head_size != kHeadDim) return kErrUnsupportedHeadDim;
   if (num_tokens < 0 || num_requests < 0 || num_heads <= 0 || num_kv_heads <= 0 ||
       num_kv_heads > kMaxInlineItems || num_heads % num_kv_heads != 0 || max_query_len < 0 ||
@@ -1405,7 +1422,8 @@ int paged_decode(const float* q_rot, const float* k_new, const float* v_new, int
       block_table_cols < 0 || stage_rows < 0 || tiles_per_split < 0 || tiles_per_split > kMaxTilesPerSplit)
     return kErrInvalidArgument;
   if (num_tokens == 0 || num_requests == 0 || max_query_len == 0) return kOk;
-  DecodeArgs a{};
+  DecodeArgs& a = L.a;
+  a = DecodeArgs{};
   int rc = fill_common(a, q_rot, num_heads, num_kv_heads, head_size, k_cache, v_cache, block_size, num_pages,
                        k_stride_page, k_stride_token, k_stride_head, v_stride_page, v_stride_token, v_stride_head,
                        block_table, block_table_stride, block_table_cols, max_history, stage_owner, stage_k_image,
@@ -1433,20 +1451,35 @@ int paged_decode(const float* q_rot, const float* k_new, const float* v_new, int
   a.max_splits = (int32_t)splits;
   a.row_tiles = (max_query_len * a.group + kRows - 1) / kRows;
   if ((rc = set_split_lds()) != kOk) return rc;
+  L.orot = orot;
+  L.qsl = query_start_loc;
+  L.seqs = seq_lens;
+  L.block_table = block_table;
+  L.bt_stride = block_table_stride;
+  L.num_requests = num_requests;
+  L.max_query_len = max_query_len;
+  L.num_kv_heads = num_kv_heads;
+  L.empty = false;
+  return kOk;
+}
+
+int launch_decode(DecodeLaunch& L, hipStream_t stream) {
+  if (L.empty) return kOk;
+  DecodeArgs& a = L.a;
   // Chunks of whole requests (at most kMaxInlineItems items); each chunk's
   // partials reuse the same workspace (the merge of one chunk precedes the
   // next split in stream order).
-  const int32_t per = requests_per_launch(num_kv_heads);
-  for (int32_t c0 = 0; c0 < num_requests; c0 += per) {
-    const int32_t nreq = num_requests - c0 < per ? num_requests - c0 : per;
+  const int32_t per = requests_per_launch(L.num_kv_heads);
+  for (int32_t c0 = 0; c0 < L.num_requests; c0 += per) {
+    const int32_t nreq = L.num_requests - c0 < per ? L.num_requests - c0 : per;
     for (int32_t i = 0; i < nreq; ++i) {
-      const int32_t qa = query_start_loc[c0 + i];
-      const int32_t nq = query_start_loc[c0 + i + 1] - qa;
-      for (int32_t h = 0; h < num_kv_heads; ++h)
-        a.items[i * num_kv_heads + h] = ItemInfo{qa, nq, seq_lens[c0 + i] - nq, (int16_t)i, (int16_t)h};
+      const int32_t qa = L.qsl[c0 + i];
+      const int32_t nq = L.qsl[c0 + i + 1] - qa;
+      for (int32_t h = 0; h < L.num_kv_heads; ++h)
+        a.items[i * L.num_kv_heads + h] = ItemInfo{qa, nq, L.seqs[c0 + i] - nq, (int16_t)i, (int16_t)h};
     }
-    a.block_table = block_table ? block_table + (int64_t)c0 * block_table_stride : nullptr;
-    const unsigned nitems = (unsigned)(nreq * num_kv_heads);
+    a.block_table = L.block_table ? L.block_table + (int64_t)c0 * L.bt_stride : nullptr;
+    const unsigned nitems = (unsigned)(nreq * L.num_kv_heads);
     // The fresh partial gets a workgroup of its own when one more per item
     // still fits the resident budget, else it rides on a history split.
     a.fresh_block = (int64_t)(a.max_splits + 1) * nitems <= kResidentSplitWgs ? 1 : 0;
@@ -1454,9 +1487,30 @@ int paged_decode(const float* q_rot, const float* k_new, const float* v_new, int
     dim3 grid((unsigned)(gx > 0 ? gx : 1), nitems, (unsigned)a.row_tiles);
     hipLaunchKernelGGL(paged_decode_split_kernel, grid, dim3(256), kLdsBytes, stream, a);
     if (hipGetLastError() != hipSuccess) return kErrLaunch;
-    if ((rc = launch_merge(a, (int64_t)max_query_len * a.group, nitems, orot, stream)) != kOk) return rc;
+    const int rc = launch_merge(a, (int64_t)L.max_query_len * a.group, nitems, L.orot, stream);
+    if (rc != kOk) return rc;
   }
   return kOk;
+}
+
+int paged_decode(const float* q_rot, const float* k_new, const float* v_new, int32_t num_tokens, int32_t num_heads,
+                 int32_t num_kv_heads, int32_t head_size, const void* k_cache, const void* v_cache,
+                 int32_t block_size, int64_t num_pages, int64_t k_stride_page, int64_t k_stride_token,
+                 int64_t k_stride_head, int64_t v_stride_page, int64_t v_stride_token, int64_t v_stride_head,
+                 const int32_t* block_table, int64_t block_table_stride, int32_t block_table_cols,
+                 const int32_t* query_start_loc, const int32_t* seq_lens, int32_t num_requests,
+                 int32_t max_query_len, int64_t max_history, const int64_t* stage_owner,
+                 const void* stage_k_image, const void* stage_v_image, int32_t stage_rows, float scale,
+                 int32_t tiles_per_split, float* out, const OutRotation& orot, void* workspace,
+                 size_t workspace_size, hipStream_t stream) {
+  DecodeLaunch L;
+  const int rc = prepare_decode(L, q_rot, k_new, v_new, num_tokens, num_heads, num_kv_heads, head_size, k_cache,
+                                v_cache, block_size, num_pages, k_stride_page, k_stride_token, k_stride_head,
+                                v_stride_page, v_stride_token, v_stride_head, block_table, block_table_stride,
+                                block_table_cols, query_start_loc, seq_lens, num_requests, max_query_len,
+                                max_history, stage_owner, stage_k_image, stage_v_image, stage_rows, scale,
+                                tiles_per_split, out, orot, workspace, workspace_size);
+  return rc != kOk ? rc : launch_decode(L, stream);
 }
 
 // Device scratch of the no-allocation entry (oscar_paged_decode_noalloc):
@@ -1645,6 +1699,42 @@ int oscar_decode_only(const float* q_rot, int32_t num_heads, int32_t num_kv_head
     if ((rc = launch_merge(a, a.group, nitems, OutRotation{nullptr, nullptr, 0, 0}, stream)) != kOk) return rc;
   }
   return kOk;
+}
+
+// The short-step forward of one layer: every argument of the decode is
+// checked before the step write is enqueued, so an error enqueues nothing.
+int oscar_mtp_forward(const oscar_mtp_layer* layer, const oscar_mtp_step* step, const void* query_bf16,
+                      int64_t query_token_stride, const void* key_bf16, const void* value_bf16,
+                      int64_t kv_token_stride, void* out, int64_t out_token_stride, int32_t out_bf16,
+                      hipStream_t stream) {
+  if (!layer || !step || layer->num_heads != step->num_heads || layer->num_kv_heads != step->num_kv_heads)
+    return kErrInvalidArgument;
+  const oscar_mtp_layer& L = *layer;
+  const oscar_mtp_step& S = *step;
+  if (!L.rot_v_t || !out || out_token_stride < (int64_t)L.num_heads * kHeadDim || out_bf16 < 0 || out_bf16 > 1)
+    return kErrInvalidArgument;
+  const int32_t rows = L.stage_rows;
+  DecodeLaunch D;
+  int rc = prepare_decode(D, S.q_rot, S.k_rot, S.v_rot, S.num_tokens, L.num_heads, L.num_kv_heads, L.head_size,
+                          L.k_cache, L.v_cache, L.block_size, L.num_pages, L.k_stride_page, L.k_stride_token,
+                          L.k_stride_head, L.v_stride_page, L.v_stride_token, L.v_stride_head, S.block_table,
+                          S.block_table_stride, S.block_table_cols, S.query_start_loc, S.seq_lens, S.num_requests,
+                          S.max_query_len, S.max_history, rows > 0 ? L.stage_owner : nullptr,
+                          rows > 0 ? L.stage_k_image : nullptr, rows > 0 ? L.stage_v_image : nullptr, rows, L.scale,
+                          S.tiles_per_split, reinterpret_cast<float*>(out),
+                          OutRotation{L.rot_v_t, out, out_token_stride, out_bf16}, S.workspace, S.workspace_size);
+  if (rc != kOk) return rc;
+  rc = oscar_step_write(query_bf16, query_token_stride, key_bf16, value_bf16, kv_token_stride, S.num_tokens,
+                        L.num_heads, L.num_kv_heads, L.head_size, L.rot_k, L.rot_v, S.slot_mapping,
+                        S.query_start_loc, S.seq_lens, S.num_requests, L.k_cache, L.v_cache, L.block_size,
+                        L.num_pages, L.k_stride_page, L.k_stride_token, L.k_stride_head, L.v_stride_page,
+                        L.v_stride_token, L.v_stride_head, L.clip_index_k, L.clip_index_v,
+                        rows > 0 ? L.stage_k : nullptr, rows > 0 ? L.stage_v : nullptr,
+                        rows > 0 ? L.stage_owner : nullptr, rows > 0 ? L.stage_k_image : nullptr,
+                        rows > 0 ? L.stage_v_image : nullptr, rows, L.sink_eff, L.recent, S.q_rot, S.k_rot, S.v_rot,
+                        stream);
+  if (rc != kOk) return rc;
+  return launch_decode(D, stream);
 }
 
 }  // extern "C"

@@ -48,6 +48,7 @@ SIGNATURES = {
                                   _c_p, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_p, _c_i32, _c_i64, _c_i64, _c_i64,
                                   _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p,
                                   _c_p, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p]),
+    "oscar_mtp_forward": (_c_i32, [_c_p, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i32, _c_p]),
     "oscar_decode_only_workspace_bytes": (_c_sz, [_c_i32, _c_i32, _c_i32, _c_i64, _c_i32]),
     "oscar_decode_only": (_c_i32, [_c_p, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_i32, _c_i64, _c_i64,
                                    _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i32,
@@ -101,7 +102,15 @@ def call(name: str, *args) -> None:
         raise OscarKernelError(f"{name} failed: {STATUS.get(status, status)}")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
+    """The hipStream_t of the device's current stream (torch's own raw-stream
+    query where it exists: no Stream object is built per call)."""
+    if _raw_stream is not None:
+        idx = device.index
+        return _raw_stream(torch.cuda.current_device() if idx is None else idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 

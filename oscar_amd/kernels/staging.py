@@ -49,6 +49,20 @@ def k_image_shape(rows: int, bs: int, hk: int) -> tuple:
     return (rows, bs // 32, hk, 2 * IMAGE_HALFS)
 
 
+def check_arena(stage_k, stage_v, owner, bs: int, hk: int, d: int) -> int:
+    """Raise unless (stage_k, stage_v, owner) is an arena the kernels can
+    index from its geometry: contiguous fp32 [rows, bs, Hk, D] values and an
+    int64 [rows, bs] owner table on one device.  Returns rows."""
+    rows = owner.shape[0] if owner.ndim == 2 else -1
+    want = (rows, bs, hk, d)
+    if owner.dtype != torch.int64 or tuple(owner.shape) != (rows, bs) or not owner.is_contiguous():
+        raise ValueError(f"staging owner must be a contiguous int64 [rows, {bs}] tensor")
+    for t in (stage_k, stage_v):
+        if t.dtype != torch.float32 or tuple(t.shape) != want or not t.is_contiguous() or t.device != owner.device:
+            raise ValueError(f"staging values must be contiguous fp32 {want} tensors on the owner's device")
+    return rows
+
+
 def check_images(k_image, v_image, rows: int, bs: int, hk: int) -> None:
     """Raise unless the operand images are absent together or are contiguous
     fp16 tensors of the arena's K and V image shapes (the kernels index them
@@ -102,6 +116,7 @@ def staging_write(key, value, slot_mapping, qsl_dev, seq_dev, num_requests: int,
     if kr.stride(1) != 1 or vr.stride(0) != kr.stride(0) or vr.stride(1) != 1:
         kr, vr = kr.contiguous(), vr.contiguous()
     slots = slot_mapping.to(torch.int64).contiguous()
+    check_arena(stage_k, stage_v, owner, block_size, num_kv_heads, head_size)
     check_images(k_image, v_image, owner.shape[0], block_size, num_kv_heads)
     _lib.call("oscar_staging_write", _lib.ptr(kr), _lib.ptr(vr), kr.stride(0), _lib.ptr(slots), N,
               _lib.ptr(qsl_dev), _lib.ptr(seq_dev), num_requests, num_kv_heads, head_size, block_size,

@@ -79,3 +79,38 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "absent.so")
     with pytest.raises(_lib.OscarKernelError, match="missing"):
         _lib.load()
+
+
+def test_struct_layouts_match_the_header(tmp_path):
+    """The ctypes mirrors of the argument structs have the C compiler's field
+    offsets and sizes (a header compiled by gcc against its own declaration)."""
+    from oscar_amd.kernels import step
+
+    structs = {"oscar_mtp_layer": step.MtpLayerArgs, "oscar_mtp_step": step.MtpStepArgs}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "oscar_amd.h"', "int main(void) {"]
+    for cname, cls in structs.items():
+        lines.append(f'  printf("{cname} sizeof %zu\\n", sizeof({cname}));')
+        for field, _ in cls._fields_:
+            lines.append(f'  printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", str(HEADER.parent), str(src), "-o", str(exe)],
+                   check=True, capture_output=True, text=True)
+    got = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], check=True, capture_output=True,
+                                                              text=True).stdout.splitlines())
+    for cname, cls in structs.items():
+        assert int(got[f"{cname} sizeof"]) == ctypes.sizeof(cls), cname
+        for field, _ in cls._fields_:
+            assert int(got[f"{cname} {field}"]) == getattr(cls, field).offset, (cname, field)
+    # the mirrors name every field the header declares, in its order
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    for cname, cls in structs.items():
+        body = re.search(r"typedef struct " + cname + r" \{(.*?)\} " + cname + ";", text, flags=re.S).group(1)
+        names = []
+        for decl in body.split(";"):
+            decl = decl.strip()
+            if decl:
+                names += [re.sub(r"^.*[\s*]", "", part.strip()) for part in decl.split(",")]
+        assert names == [f for f, _ in cls._fields_], cname

@@ -351,3 +351,110 @@ def test_request_layout_is_built_once_per_step():
     assert b is not a and b.max_hist == 97
     with pytest.raises(ValueError):
         kdecode.request_layout([0, 4, 5], [3, 7])         # history would be negative
+
+
+class _RecordingLib:
+    """The real library for its host-only size queries; the MTP forward entry
+    replaced by a recorder (no kernel is called without a GPU)."""
+
+    def __init__(self, real):
+        self._real = real
+        self.calls = []
+
+    def __getattr__(self, name):
+        return getattr(self._real, name)
+
+    def oscar_mtp_forward(self, layer, st, q, qs, k, v, ks, out, os_, bf16, stream):
+        self.calls.append(dict(layer=layer, step=st, q=q, qs=qs, k=k, v=v, ks=ks, out=out, os=os_, bf16=bf16))
+        return 0
+
+
+def _short_step_setup(clean_env, monkeypatch):
+    from oscar_amd.kernels import _lib, step as kstep
+
+    real = _lib.load()
+    fake = _RecordingLib(real)
+    monkeypatch.setattr(_lib, "_lib", fake)
+    monkeypatch.setattr(_lib, "stream_handle", lambda dev: 1234)
+    monkeypatch.setattr(kstep, "_LAST_STEP", [None])
+    impls, layers = [], []
+    for i in range(2):
+        impl = make_impl(clean_env)
+        layer = NS(layer_name=f"model.layers.{i}.self_attn.attn")
+        rk, rv = torch.eye(256), torch.eye(256)
+        layer._oscar_rots = (rk, rv)
+        layer._oscar_rot_ops = (rk, rv, None, None)
+        layer._oscar_rvT = rv.t().contiguous()
+        impls.append(impl)
+        layers.append(layer)
+    caches = [[torch.zeros(8, 128, 1, 256, dtype=torch.int8) for _ in range(2)] for _ in range(2)]
+    return fake, impls, layers, caches
+
+
+def _short_md(seqs, qlens):
+    qsl = [0]
+    for n in qlens:
+        qsl.append(qsl[-1] + n)
+    N = qsl[-1]
+    return NS(num_actual_tokens=N, slot_mapping=torch.arange(N, dtype=torch.int64),
+              query_start_loc_cpu=torch.tensor(qsl, dtype=torch.int32), seq_lens_list=list(seqs),
+              block_tables=torch.zeros(len(seqs), 8, dtype=torch.int32), attn_state=None)
+
+
+def test_short_step_packs_layer_and_step_halves_once(clean_env, monkeypatch):
+    """Every layer of a short step makes one oscar_mtp_forward call; the
+    layers share the step half, and each layer's half is packed once and
+    reused by the next step."""
+    fake, impls, layers, caches = _short_step_setup(clean_env, monkeypatch)
+    md = _short_md([300, 41], [4, 1])
+    q = torch.zeros(7, 6 * 256, dtype=torch.bfloat16)       # 2 padding rows
+    kv = torch.zeros(7, 3 * 256, dtype=torch.bfloat16)      # k | v | pad columns of a fused projection
+    k, v = kv[:, :256], kv[:, 256:512]
+    outs = [torch.full((7, 6 * 256), 3.0, dtype=torch.bfloat16) for _ in range(2)]
+    for impl, layer, c, out in zip(impls, layers, caches, outs):
+        impl.forward(layer, q, k, v, c, md, output=out)
+    assert len(fake.calls) == 2
+    a, b = fake.calls
+    assert a["step"] == b["step"] and a["layer"] != b["layer"]
+    assert a["qs"] == 6 * 256 and a["ks"] == 3 * 256 and a["v"] == v.data_ptr() and a["bf16"] == 1
+    assert a["out"] == outs[0].data_ptr() and a["os"] == 6 * 256
+    for out in outs:
+        assert (out[5:] == 0).all() and (out[:5] == 3.0).all()   # padding rows cleared, the rest left to the kernel
+    # The next step: new lengths build a new step half; the layer halves stay.
+    md2 = _short_md([301, 42], [1, 1])
+    for impl, layer, c, out in zip(impls, layers, caches, outs):
+        impl.forward(layer, q, k, v, c, md2, output=out)
+    c, d = fake.calls[2:]
+    assert c["step"] == d["step"] != a["step"]
+    assert c["layer"] == a["layer"] and d["layer"] == b["layer"]
+    # A rebound cache rebuilds that layer's half.
+    caches[0] = [t.clone() for t in caches[0]]
+    impls[0].forward(layers[0], q, k, v, caches[0], md2, output=outs[0])
+    assert fake.calls[-1]["layer"] != a["layer"] and fake.calls[-1]["step"] == c["step"]
+
+
+def test_short_step_routing_and_capture(clean_env, monkeypatch):
+    """A request longer than 16 tokens leaves the short route; under a
+    declared fixed-step capture every call builds its own step half (its
+    scratch then belongs to the graph)."""
+    fake, impls, layers, caches = _short_step_setup(clean_env, monkeypatch)
+    impl, layer, c = impls[0], layers[0], caches[0]
+    q = torch.zeros(17, 6 * 256, dtype=torch.bfloat16)
+    k = torch.zeros(17, 256, dtype=torch.bfloat16)
+    out = torch.zeros(17, 6 * 256, dtype=torch.bfloat16)
+    impl._set_caches(c)
+    assert impl._short_step(layer, q, k, k, c, _short_md([300], [17]), out, False) is False
+    assert fake.calls == []
+    from oscar_amd.kernels import step as kstep
+
+    built = []
+    init = kstep.MtpStep.__init__
+    monkeypatch.setattr(kstep.MtpStep, "__init__", lambda self, *a: (built.append(1), init(self, *a))[1])
+    monkeypatch.setattr(kstep, "_LAST_STEP", [None])
+    md = _short_md([300], [4])
+    assert impl._short_step(layer, q, k, k, c, md, out, True) is True
+    assert impl._short_step(layer, q, k, k, c, md, out, True) is True
+    assert len(built) == 2 and kstep._LAST_STEP[0] is None and len(fake.calls) == 2
+    assert impl._short_step(layer, q, k, k, c, md, out, False) is True
+    assert impl._short_step(layer, q, k, k, c, md, out, False) is True
+    assert len(built) == 3 and fake.calls[2]["step"] == fake.calls[3]["step"]
