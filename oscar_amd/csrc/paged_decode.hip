@@ -645,16 +645,15 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
           for (int aa = 0; aa < 2; ++aa)
             ka[aa] = wl ? __builtin_bit_cast(half8, im[2 * j + aa]) : ka[aa];
           qk_pair(j, ka[0], ka[1]);
-          // Once a half of the high part is used, its registers take the same
-          // half of the low part, zero for lanes of tokens outside the window
-          // (the barriers keep the loads from moving up, where they would
-          // need registers of their own).
-          if (j == 3 || j == 7) {
-            __builtin_amdgcn_sched_barrier(0);
+          // As soon as a k-step pair of the high part is used, its registers
+          // take the same pair of the low part, zero for lanes of tokens
+          // outside the window, so the first low loads have the rest of the
+          // high pass to arrive (the barriers keep the loads from moving up,
+          // where they would need registers of their own).
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int m = 0; m < 8; ++m) im[m + (j - 3) * 2] = wl ? img_lo[(m + (j - 3) * 2) * 64 + lane] : u32x4{};
-            __builtin_amdgcn_sched_barrier(0);
-          }
+          for (int m = 2 * j; m < 2 * j + 2; ++m) im[m] = wl ? img_lo[m * 64 + lane] : u32x4{};
+          __builtin_amdgcn_sched_barrier(0);
         }
         // window tokens (the other lanes hold zeros): low part of k against
         // the high part of q (the low-low product is below 2^-22 of the
