@@ -273,7 +273,7 @@ __global__ __launch_bounds__(256) void quant_write_prerotated_kernel(
 //   128*(l >> 5) + 16*T + i of token (l & 31) -- the per-lane layout above.
 // grid = (ceil(N / 128), Hk * 2), block = 256 (4 waves x 32 tokens; two
 // blocks per CU).  The 16 K-step chunks (16 KB each) stream through a 4-slot
-// LDS ring filled with global_load_lds_dwordx4: chunk m + 3 is requested
+// LDS ring filled with buffer_load_dwordx4 ... lds: chunk m + 3 is requested
 // while chunk m is multiplied, into the slot chunk m - 1 left.  Each K step
 // issues the 8 tiles' hi passes, then their lo passes, so no MFMA waits on the
 // previous.
@@ -347,13 +347,20 @@ __global__ __launch_bounds__(256, 2) void quant_write_fused_kernel(
   bf16x8 xlo[8], xhi[8];
 #pragma unroll
   for (int m = 0; m < 8; ++m) xlo[m] = load_x(m);
-  // Thread's share of a chunk: wave w copies 1 KB blocks 4w .. 4w + 3.
+  // Thread's share of a chunk: wave w copies 1 KB blocks 4w .. 4w + 3.  The
+  // copies are buffer loads: unlike the flat-encoded global form, they count
+  // only in vmcnt, so the operand reads from LDS below keep a partial
+  // lgkmcnt wait each instead of draining every outstanding LDS read.
+  typedef __attribute__((address_space(3))) void lds_void;
+  const __amdgpu_buffer_rsrc_t rop_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)rop, (short)0, (int)(kSteps * kChunkBytes), 0x00020000);
   auto request = [&](int chunk) {
 #pragma unroll
     for (int i = 0; i < kDmaPerChunk; ++i) {
       const int blk = kDmaPerChunk * wave + i;
-      __builtin_amdgcn_global_load_lds(rop + (size_t)chunk * kChunkBytes + (blk * 64 + lane) * 16,
-                                       ring + (chunk % kRing) * kChunkBytes + blk * 1024, 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rop_rsrc, (lds_void*)(uintptr_t)(uint32_t)(uintptr_t)(ring + (chunk % kRing) * kChunkBytes + blk * 1024),
+          16, chunk * kChunkBytes + (blk * 64 + lane) * 16, 0, 0, 0);
     }
   };
   request(0);
