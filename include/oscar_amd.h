@@ -40,7 +40,8 @@ enum oscar_status {
  * (x_rot = x @ R).  Replaces the reference's per-call fp32 matmul operand
  * (oscar_ascend/backend.py:130 `torch.matmul(x.float(), R)`, rotations cached
  * per layer at backend.py:228-236).  `operand` must hold
- * oscar_rotation_operand_bytes(D) bytes (bf16 hi + lo split, permuted).
+ * oscar_rotation_operand_bytes(D) bytes: the MFMA tiles (bf16 hi + lo split,
+ * permuted, 256 KiB), then R itself in fp32 (256 KiB) for short writes.
  */
 size_t oscar_rotation_operand_bytes(int32_t head_size);
 int oscar_rotation_operand(const float* rotation, void* operand, int32_t head_size,
@@ -57,6 +58,8 @@ int oscar_rotation_operand(const float* rotation, void* operand, int32_t head_si
  *                         at or beyond num_pages * block_size);
  *   clip_index_*:         sorted-|x| index of the clip threshold
  *                         (min(int(ratio * D), D - 1)), or -1 for no clip.
+ * Writes of at most 2048 vectors (2 * num_tokens * num_kv_heads) rotate in
+ * fp32 through oscar_step_write's kernel; larger ones on MFMA.
  */
 int oscar_quant_write(const void* key_bf16, const void* value_bf16, int64_t num_tokens,
                       int32_t num_kv_heads, int32_t head_size, int64_t token_stride,
@@ -240,6 +243,8 @@ int oscar_prefill_continuation(const float* q_rot, const float* k_new, const flo
  *   query_start_loc [num_requests + 1], seq_lens [num_requests] in HOST memory
  *     (token t of request i sits at seq_lens[i] - query_start_loc[i + 1] + t);
  *   q_rot [num_tokens][Hq][D], k_rot / v_rot [num_tokens][Hk][D] fp32 outputs.
+ * num_heads = 0 writes keys and values only (query_bf16 and q_rot unused);
+ * a null k_rot / v_rot skips that output.
  */
 int oscar_step_write(const void* query_bf16, int64_t query_token_stride, const void* key_bf16,
                      const void* value_bf16, int64_t kv_token_stride, int32_t num_tokens,

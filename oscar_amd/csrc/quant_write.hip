@@ -282,6 +282,12 @@ constexpr int kFusedWaves = 4;
 constexpr int kChunkBytes = 2 * 8 * 64 * 16;   // one K step: 2 passes x 8 tiles x 64 lanes x 16 B
 constexpr int kRing = 4;
 constexpr int kSteps = 16;
+// The rotation operand: the MFMA tiles (kSteps chunks, bf16 hi + lo), then R
+// itself in fp32 (row-major), which short writes rotate with.
+constexpr int kMfmaEntries = kSteps * kChunkBytes / 2;
+constexpr size_t kMfmaOperandBytes = (size_t)kSteps * kChunkBytes;
+constexpr size_t kOperandBytes = kMfmaOperandBytes + sizeof(float) * kHeadDim * kHeadDim;
+constexpr int64_t kShortWriteVectors = 2048;   // at most 1024 tokens (the step write's limit)
 constexpr int kDmaPerChunk = kChunkBytes / (kFusedWaves * 64 * 16);   // 2 per thread
 constexpr size_t kFusedLds = kFusedWaves * sizeof(SelLds) > kRing * kChunkBytes
                                  ? kFusedWaves * sizeof(SelLds) : (size_t)kRing * kChunkBytes;
@@ -424,10 +430,15 @@ __global__ __launch_bounds__(256, 2) void quant_write_fused_kernel(
   quantize_store(v, p, live ? slots[tok] : -1, head, side, half, c);
 }
 
-// One thread per operand element (2 x 16 x 8 x 64 x 8 = 131072 entries).
+// One thread per operand element (2 x 16 x 8 x 64 x 8 = 131072 entries), then
+// one per element of the fp32 copy of R that follows them (65536 entries).
 __global__ void rotation_operand_kernel(const float* __restrict__ R, __bf16* __restrict__ out) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= 2 * 16 * 8 * 64 * 8) return;
+  if (idx >= kMfmaEntries) {
+    if (idx < kMfmaEntries + kHeadDim * kHeadDim)
+      reinterpret_cast<float*>(out + kMfmaEntries)[idx - kMfmaEntries] = R[idx - kMfmaEntries];
+    return;
+  }
   const int u = idx & 7;
   const int lane = (idx >> 3) & 63;
   const int t = (idx >> 9) & 7;
@@ -464,15 +475,27 @@ using namespace oscar;
 
 extern "C" {
 
+// step_write.hip: the short-step write, used here without a query or window.
+int oscar_step_write(const void* query_bf16, int64_t query_token_stride, const void* key_bf16,
+                     const void* value_bf16, int64_t kv_token_stride, int32_t num_tokens, int32_t num_heads,
+                     int32_t num_kv_heads, int32_t head_size, const float* rot_k, const float* rot_v,
+                     const int64_t* slot_mapping, const int32_t* query_start_loc, const int32_t* seq_lens,
+                     int32_t num_requests, void* k_cache, void* v_cache, int32_t block_size, int64_t num_pages,
+                     int64_t k_stride_page, int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
+                     int64_t v_stride_token, int64_t v_stride_head, int32_t clip_index_k, int32_t clip_index_v,
+                     float* stage_k, float* stage_v, int64_t* stage_owner, void* stage_k_image,
+                     void* stage_v_image, int32_t stage_rows, int32_t sink_eff, int32_t recent, float* q_rot,
+                     float* k_rot, float* v_rot, hipStream_t stream);
+
 size_t oscar_rotation_operand_bytes(int32_t head_size) {
-  return head_size == kHeadDim ? (size_t)16 * kChunkBytes : 0;
+  return head_size == kHeadDim ? kOperandBytes : 0;
 }
 
 int oscar_rotation_operand(const float* rotation, void* operand, int32_t head_size,
                            hipStream_t stream) {
   if (head_size != kHeadDim) return kErrUnsupportedHeadDim;
   if (rotation == nullptr || operand == nullptr) return kErrInvalidArgument;
-  const int total = 2 * 16 * 8 * 64 * 8;
+  const int total = kMfmaEntries + kHeadDim * kHeadDim;
   hipLaunchKernelGGL(rotation_operand_kernel, dim3((total + 255) / 256), dim3(256), 0, stream,
                      rotation, static_cast<__bf16*>(operand));
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
@@ -530,6 +553,20 @@ int oscar_quant_write(const void* key_bf16, const void* value_bf16, int64_t num_
               block_size, num_pages * (int64_t)block_size, FastDiv{}};
   int st = check_cache_args(c);
   if (st != kOk) return st;
+  // Short writes (at most kShortWriteVectors key + value vectors): the fp32
+  // rotation of the short-step write, one workgroup per vector reading R
+  // from the operand's fp32 copy, instead of a 128-token MFMA tile that
+  // streams the whole operand through one CU's LDS for a few tokens.
+  if (2 * num_tokens * num_kv_heads <= kShortWriteVectors) {
+    const uint8_t* ok = static_cast<const uint8_t*>(rot_k_operand) + kMfmaOperandBytes;
+    const uint8_t* ov = static_cast<const uint8_t*>(rot_v_operand) + kMfmaOperandBytes;
+    return oscar_step_write(nullptr, 0, key_bf16, value_bf16, token_stride, (int32_t)num_tokens, 0, num_kv_heads,
+                            head_size, reinterpret_cast<const float*>(ok), reinterpret_cast<const float*>(ov),
+                            slot_mapping, nullptr, nullptr, 0, k_cache, v_cache, block_size, num_pages,
+                            k_stride_page, k_stride_token, k_stride_head, v_stride_page, v_stride_token,
+                            v_stride_head, clip_index_k, clip_index_v, nullptr, nullptr, nullptr, nullptr,
+                            nullptr, 0, 0, 0, nullptr, nullptr, nullptr, stream);
+  }
   if (set_dynamic_lds(reinterpret_cast<const void*>(quant_write_fused_kernel), (int)kFusedLds, g_lds_set) != kOk) return kErrLaunch;
   const int64_t per_block = kFusedWaves * kTokPerWave;
   dim3 grid((unsigned)((num_tokens + per_block - 1) / per_block), (unsigned)(num_kv_heads * 2));

@@ -360,7 +360,7 @@ __global__ __launch_bounds__(kThreads) void step_write_kernel(StepArgs a) {
   }
   const int e = e0 + w, t = e / heads, h = e - t * heads;
   float* out = side == 0 ? c.k_rot : (side == 1 ? c.v_rot : c.q_rot);
-  *reinterpret_cast<floatx4*>(out + ((int64_t)t * heads + h) * kHeadDim + 4 * lane) = y;
+  if (out != nullptr) *reinterpret_cast<floatx4*>(out + ((int64_t)t * heads + h) * kHeadDim + 4 * lane) = y;
   if (side < 2) write_vector(ctx, y, t, h, side, lane, my_slot, later, keep_word);
 }
 
@@ -381,13 +381,13 @@ extern "C" int oscar_step_write(const void* query_bf16, int64_t query_token_stri
                                 void* stage_k_image, void* stage_v_image, int32_t stage_rows, int32_t sink_eff,
                                 int32_t recent, float* q_rot, float* k_rot, float* v_rot, hipStream_t stream) {
   if (head_size != kHeadDim) return kErrUnsupportedHeadDim;
-  if (num_tokens < 0 || num_tokens > kMaxStepTokens || num_requests < 0 || num_heads <= 0 ||
+  if (num_tokens < 0 || num_tokens > kMaxStepTokens || num_requests < 0 || num_heads < 0 ||
       num_kv_heads <= 0 || num_heads % num_kv_heads != 0 || block_size <= 0 || num_pages <= 0 ||
       stage_rows < 0 || sink_eff < 0 || recent < 0 || clip_index_k >= kHeadDim || clip_index_v >= kHeadDim)
     return kErrInvalidArgument;
   if (num_tokens == 0) return kOk;
-  if (!query_bf16 || !key_bf16 || !value_bf16 || !rot_k || !rot_v || !slot_mapping || !k_cache || !v_cache ||
-      !q_rot || !k_rot || !v_rot || (num_requests > 0 && (!query_start_loc || !seq_lens)))
+  if (!key_bf16 || !value_bf16 || !rot_k || !rot_v || !slot_mapping || !k_cache || !v_cache ||
+      (num_heads > 0 && (!query_bf16 || !q_rot)) || (num_requests > 0 && (!query_start_loc || !seq_lens)))
     return kErrInvalidArgument;
   if (query_token_stride < (int64_t)num_heads * kHeadDim || kv_token_stride < (int64_t)num_kv_heads * kHeadDim)
     return kErrInvalidArgument;

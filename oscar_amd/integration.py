@@ -23,7 +23,7 @@ from copy import deepcopy
 from pathlib import Path
 
 MI355X_HBM_BYTES = 288 * 10 ** 9
-ROTATION_OPERAND_BYTES = 262144        # oscar_rotation_operand_bytes(256)
+ROTATION_OPERAND_BYTES = 524288        # oscar_rotation_operand_bytes(256): MFMA tiles + fp32 R
 
 
 def memory_budget(available: int, native_per_block: int, shadow_per_block: int, fixed_bytes: int) -> int:

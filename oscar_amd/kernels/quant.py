@@ -36,7 +36,8 @@ def _check_device(*tensors):
 
 
 def rotation_operand(R: torch.Tensor) -> torch.Tensor:
-    """MFMA operand of rotation R [D, D] (x_rot = x @ R), uint8 bytes on R's device."""
+    """Operand of rotation R [D, D] (x_rot = x @ R), uint8 bytes on R's device:
+    the MFMA tiles (bf16 high + low parts), then R in fp32 for short writes."""
     D = R.shape[0]
     check_d(D)
     if R.shape != (D, D):
@@ -83,7 +84,8 @@ def quant_write_prerotated(k_rot, v_rot, k_cache, v_cache, slot_mapping, clip_k:
 
 def quant_write(key, value, rot_k_op, rot_v_op, k_cache, v_cache, slot_mapping, clip_k: int,
                 clip_v: int, num_kv_heads: int, head_size: int) -> None:
-    """Fused rotate (MFMA) + clip + quantize + pack + write of bf16 K/V."""
+    """Fused rotate + clip + quantize + pack + write of bf16 K/V: the rotation
+    runs on MFMA, or in fp32 for writes of at most 2048 key + value vectors."""
     N = slot_mapping.shape[0]
     if N == 0:
         return

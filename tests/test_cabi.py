@@ -62,7 +62,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_size_queries(lib):
-    assert lib.oscar_rotation_operand_bytes(256) == 262144
+    assert lib.oscar_rotation_operand_bytes(256) == 524288
     assert lib.oscar_rotation_operand_bytes(128) == 0
     assert lib.oscar_paged_decode_workspace_bytes(0, 1, 6, 4, 100, 0) == 0
     assert lib.oscar_paged_decode_workspace_bytes(1, 2, 5, 4, 100, 0) == 0     # Hq % Hk

@@ -127,13 +127,17 @@ def test_prerotated_large_random_write(device):
         assert torch.equal(got.cpu().view(torch.uint8), want.view(torch.uint8))
 
 
-@pytest.mark.parametrize("hk", [1, 2])
-def test_fused_rotation_within_tolerance(device, hk):
-    N, bs, pages = 1000, 128, 9
+@pytest.mark.parametrize("N,hk", [(1, 1), (4, 1), (128, 1), (1000, 1), (512, 2), (1025, 1), (1000, 2)])
+def test_fused_rotation_within_tolerance(device, N, hk):
+    """Writes of at most 2048 key + value vectors (N x Hk up to 1000 x 1 and
+    512 x 2) take the fp32 short path, larger ones (1025 x 1, 1000 x 2) the
+    MFMA one."""
+    bs = 128
+    pages = N // bs + 2
     k, v = synthetic.kv(N, hk, D, seed=13)
     Rk, Rv = synthetic.rotations(D, seed=17)
     slots = torch.randperm(pages * bs, generator=torch.Generator().manual_seed(2))[:N].to(torch.int64)
-    slots[::11] = -1
+    slots[1::11] = -1
     caches = [torch.zeros(pages, bs, hk, D, dtype=torch.int8) for _ in range(2)]
     k_rot = orot.rotate_clip(k, Rk, 0.0)
     v_rot = orot.rotate_clip(v, Rv, 0.0)
@@ -252,3 +256,50 @@ def test_fused_exact_rotation_bit_exact(device, idx):
             g8, w8 = zero_sign_free(g8), zero_sign_free(w8)
         bad = (g8 != w8).reshape(pages * bs, -1).any(-1)
         assert not bad.any(), f"slots {bad.nonzero().flatten()[:8].tolist()} differ at idx {idx}"
+
+
+@pytest.mark.parametrize("N,hk", [(1, 1), (7, 2), (64, 2), (1024, 1)])
+@pytest.mark.parametrize("idx", [-1, 0, 235, 255])
+def test_short_write_exact_rotation_bit_exact(device, N, hk, idx):
+    """The short path of the fused entry (at most 2048 key + value vectors,
+    fp32 rotation from the operand's copy of R) with R a signed permutation:
+    every rotated value is exact, so cache bytes match the oracle byte for
+    byte, including skipped slots and the clip search at the edge ranks."""
+    base = torch.cat([_threshold_cases(53), torch.randn(32, D) * 2.0])
+    g = torch.Generator().manual_seed(1000 * N + 10 * hk + idx)
+    pick = torch.randint(0, base.shape[0], (2, N * hk), generator=g)
+    k = base[pick[0]].reshape(N, hk, D).to(torch.bfloat16)
+    v = base[pick[1]].reshape(N, hk, D).to(torch.bfloat16)
+    Rs = []
+    for _ in range(2):
+        perm = torch.randperm(D, generator=g)
+        sign = torch.where(torch.rand(D, generator=g) < 0.5, -1.0, 1.0)
+        R = torch.zeros(D, D)
+        R[torch.arange(D), perm] = sign
+        Rs.append(R)
+    bs = 16
+    pages = N // bs + 3
+    slots = torch.randperm(pages * bs, generator=g)[:N].to(torch.int64)
+    if N > 1:
+        slots[::5] = -1
+    ratio = 0.0 if idx < 0 else (idx + 0.5) / D
+    caches = make_caches(pages, bs, hk, torch.int8, seed=9)
+    expect = oracle_store(k.float() @ Rs[0], v.float() @ Rs[1], caches, slots, ratio, ratio)
+    dev = [c.to(device) for c in caches]
+    ops = [quant.rotation_operand(R.to(device)) for R in Rs]
+    quant.quant_write(k.to(device), v.to(device), ops[0], ops[1], dev[0], dev[1], slots.to(device), idx, idx, hk, D)
+    torch.cuda.synchronize()
+    for i, (got, want) in enumerate(zip(dev, expect)):
+        g8, w8 = got.cpu().view(torch.uint8), want.view(torch.uint8)
+        if i == 0:
+            g8, w8 = zero_sign_free(g8), zero_sign_free(w8)
+        bad = (g8 != w8).reshape(pages * bs, -1).any(-1)
+        assert not bad.any(), f"slots {bad.nonzero().flatten()[:8].tolist()} differ at idx {idx}"
+
+
+def test_rotation_operand_holds_fp32_copy(device):
+    """The operand's second half is R itself (fp32, row-major)."""
+    R = synthetic.rotations(D, seed=3)[0]
+    op = quant.rotation_operand(R.to(device)).cpu()
+    assert op.numel() == 2 * 262144
+    assert torch.equal(op[262144:].view(torch.float32).reshape(D, D), R.float())
