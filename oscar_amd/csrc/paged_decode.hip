@@ -386,6 +386,17 @@ __device__ __forceinline__ T pick4(T v0, T v1, T v2, T v3, int i) {
   return i == 0 ? v0 : (i == 1 ? v1 : (i == 2 ? v2 : v3));
 }
 
+// kMidIssue selects where the step loop requests the next step's loads: at
+// the top of the step (false), or after the step's score pass (true), where
+// every image load of the step has been issued before them.  Loads complete
+// in issue order and the compiler cannot tell which of a step's conditional
+// image loads a path really issued, so at the top it makes the window-free
+// path wait for the next step's loads before its score pass; after the score
+// pass they are newer than every image load.  The single-step workgroups
+// (long-history MTP reads such as 1 x 4 tokens over 24K) run the first
+// instance, whose allocation was tuned for their window tiles; multi-step
+// launches run the second (C3 55.1 -> 54.0 us, C5 38.5 -> 37.7 us).
+template <bool kMidIssue>
 __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
   // History splits are dispatched as 0, S - 1, S - 2, ..., 1: the first and
@@ -534,7 +545,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   const uint32_t e2 = 2u * (uint32_t)(col & 1);
   const uint32_t ls0 = 8u - e2, rs0 = e2, ls1 = 4u - e2, rs1 = 4u + e2;
 
-  auto run_step = [&](const StepLoad& L, int k, const int (&pgs)[kWaves]) {
+  auto run_step = [&](const StepLoad& L, int k, const int (&pgs)[kWaves], auto&& issue_next) {
     const int tbase = (split + nsplit * k) * kStepTok;
     StepLds& B = S.buf[k & 1];
     // window-owned tokens of the step's four tiles (bit t of wmj: token t of tile j)
@@ -686,6 +697,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
         }
       }
     }
+    issue_next();
     // scores (lane: row col, tokens 8 (r / 4) + 4g + r % 4) and the tile's row max
     float mb = -__builtin_inff();
 #pragma unroll
@@ -801,19 +813,28 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   };
 
   // Steady state: the next step's loads are issued before this step's are
-  // used, unconditionally, so each wait counts exactly one step's loads.
+  // used (at the top of the step or after its score pass), unconditionally,
+  // so each wait counts exactly one step's loads.
   int k = 0;
 #pragma unroll 1
   for (; k + 1 < nst; ++k) {
     int pgn[kWaves];
-    step_pages(k + 1, pgn);
-    const StepLoad nxt = load_step(a, pgn, (split + nsplit * (k + 1)) * kStepTok, prefix, kvh, w, lane);
-    run_step(cur, k, pg);
+    StepLoad nxt;
+    auto issue = [&] {
+      step_pages(k + 1, pgn);
+      nxt = load_step(a, pgn, (split + nsplit * (k + 1)) * kStepTok, prefix, kvh, w, lane);
+    };
+    if constexpr (kMidIssue) {
+      run_step(cur, k, pg, issue);
+    } else {
+      issue();
+      run_step(cur, k, pg, [] {});
+    }
     cur = nxt;
 #pragma unroll
     for (int j = 0; j < kWaves; ++j) pg[j] = pgn[j];
   }
-  run_step(cur, k, pg);
+  run_step(cur, k, pg, [] {});
 
   // ---- row sums over both lane halves and the four waves, then the partial ----
   // The sums go through the Q^T area, which no wave reads after the last
@@ -1325,10 +1346,28 @@ int fill_common(DecodeArgs& a, const float* q_rot, int32_t num_heads, int32_t nu
   return kOk;
 }
 
-std::atomic<uint64_t> g_split_lds_set{0};
+std::atomic<uint64_t> g_split_lds_set[2] = {{0}, {0}};
 
 int set_split_lds() {
-  return set_dynamic_lds(reinterpret_cast<const void*>(paged_decode_split_kernel), (int)kLdsBytes, g_split_lds_set);
+  const int rc = set_dynamic_lds(reinterpret_cast<const void*>(paged_decode_split_kernel<false>), (int)kLdsBytes,
+                                 g_split_lds_set[0]);
+  if (rc != kOk) return rc;
+  return set_dynamic_lds(reinterpret_cast<const void*>(paged_decode_split_kernel<true>), (int)kLdsBytes,
+                         g_split_lds_set[1]);
+}
+
+// Split kernel instance of a launch chunk: the mid-step load issue when some
+// item has more 128-token steps than there are splits.
+void launch_split(const DecodeArgs& a, unsigned nitems, dim3 grid, hipStream_t stream) {
+  bool multi = false;
+  for (unsigned i = 0; i < nitems; ++i) {
+    const int64_t steps = ((int64_t)a.items[i].prefix + kStepTok - 1) / kStepTok;
+    if (a.items[i].nq > 0 && steps > a.max_splits) multi = true;
+  }
+  if (multi)
+    hipLaunchKernelGGL(paged_decode_split_kernel<true>, grid, dim3(256), kLdsBytes, stream, a);
+  else
+    hipLaunchKernelGGL(paged_decode_split_kernel<false>, grid, dim3(256), kLdsBytes, stream, a);
 }
 
 // Merge blocks per feature quarter: one per row of a row tile that can hold
@@ -1484,7 +1523,7 @@ int launch_decode(DecodeLaunch& L, hipStream_t stream) {
     a.fresh_block = (int64_t)(a.max_splits + 1) * nitems <= kResidentSplitWgs ? 1 : 0;
     const int gx = a.max_splits + a.fresh_block;
     dim3 grid((unsigned)(gx > 0 ? gx : 1), nitems, (unsigned)a.row_tiles);
-    hipLaunchKernelGGL(paged_decode_split_kernel, grid, dim3(256), kLdsBytes, stream, a);
+    launch_split(a, nitems, grid, stream);
     if (hipGetLastError() != hipSuccess) return kErrLaunch;
     const int rc = launch_merge(a, (int64_t)L.max_query_len * a.group, nitems, L.orot, stream);
     if (rc != kOk) return rc;
@@ -1692,7 +1731,7 @@ int oscar_decode_only(const float* q_rot, int32_t num_heads, int32_t num_kv_head
     }
     if (a.max_splits > 0) {
       dim3 grid((unsigned)a.max_splits, nitems, (unsigned)a.row_tiles);
-      hipLaunchKernelGGL(paged_decode_split_kernel, grid, dim3(256), kLdsBytes, stream, a);
+      launch_split(a, nitems, grid, stream);
       if (hipGetLastError() != hipSuccess) return kErrLaunch;
     }
     if ((rc = launch_merge(a, a.group, nitems, OutRotation{nullptr, nullptr, 0, 0}, stream)) != kOk) return rc;
