@@ -23,6 +23,7 @@
 // producer wave and a consumer wave share each SIMD, so dequantization
 // overlaps the MFMAs.
 #include "oscar_common.h"
+#include "../../include/oscar_amd.h"
 
 namespace oscar {
 namespace {

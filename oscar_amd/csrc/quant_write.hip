@@ -21,6 +21,7 @@
 //
 // Quantization: the exact divide-free thresholds of int2_quant.h.
 #include "int2_quant.h"
+#include "../../include/oscar_amd.h"
 
 namespace oscar {
 namespace {
@@ -474,18 +475,6 @@ std::atomic<uint64_t> g_lds_set{0};   // dynamic-LDS attribute set, one bit per 
 using namespace oscar;
 
 extern "C" {
-
-// step_write.hip: the short-step write, used here without a query or window.
-int oscar_step_write(const void* query_bf16, int64_t query_token_stride, const void* key_bf16,
-                     const void* value_bf16, int64_t kv_token_stride, int32_t num_tokens, int32_t num_heads,
-                     int32_t num_kv_heads, int32_t head_size, const float* rot_k, const float* rot_v,
-                     const int64_t* slot_mapping, const int32_t* query_start_loc, const int32_t* seq_lens,
-                     int32_t num_requests, void* k_cache, void* v_cache, int32_t block_size, int64_t num_pages,
-                     int64_t k_stride_page, int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
-                     int64_t v_stride_token, int64_t v_stride_head, int32_t clip_index_k, int32_t clip_index_v,
-                     float* stage_k, float* stage_v, int64_t* stage_owner, void* stage_k_image,
-                     void* stage_v_image, int32_t stage_rows, int32_t sink_eff, int32_t recent, float* q_rot,
-                     float* k_rot, float* v_rot, hipStream_t stream);
 
 size_t oscar_rotation_operand_bytes(int32_t head_size) {
   return head_size == kHeadDim ? kOperandBytes : 0;

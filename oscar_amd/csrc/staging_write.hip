@@ -14,6 +14,7 @@
 //
 // A kept winner also refreshes the fp16 operand images of window_images.h.
 #include "window_images.h"
+#include "../../include/oscar_amd.h"
 
 namespace oscar {
 namespace {

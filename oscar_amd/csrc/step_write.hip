@@ -26,6 +26,7 @@
 // writes the slot and, when it is its seat's winner, the window.
 #include "int2_quant.h"
 #include "window_images.h"
+#include "../../include/oscar_amd.h"
 
 namespace oscar {
 namespace {
