@@ -303,3 +303,39 @@ def test_rotation_operand_holds_fp32_copy(device):
     op = quant.rotation_operand(R.to(device)).cpu()
     assert op.numel() == 2 * 262144
     assert torch.equal(op[262144:].view(torch.float32).reshape(D, D), R.float())
+
+
+@pytest.mark.parametrize("cache_dtype", [torch.int8, torch.bfloat16])
+def test_short_write_geometry_and_out_of_range_slots(device, cache_dtype):
+    """Short path (here 3 tokens x 4 kv heads) over int8 and bf16 cache
+    geometries, with a slot beyond the cache and a skipped one: bytes match
+    the oracle store everywhere (an exact rotation keeps every rotated value
+    exact), so nothing outside the valid slots is written."""
+    N, hk, bs, pages = 3, 4, 16, 2
+    g = torch.Generator().manual_seed(77)
+    base = torch.cat([_threshold_cases(59), torch.randn(16, D)])
+    pick = torch.randint(0, base.shape[0], (2, N * hk), generator=g)
+    k = base[pick[0]].reshape(N, hk, D).to(torch.bfloat16)
+    v = base[pick[1]].reshape(N, hk, D).to(torch.bfloat16)
+    Rs = []
+    for _ in range(2):
+        perm = torch.randperm(D, generator=g)
+        sign = torch.where(torch.rand(D, generator=g) < 0.5, -1.0, 1.0)
+        R = torch.zeros(D, D)
+        R[torch.arange(D), perm] = sign
+        Rs.append(R)
+    slots = torch.tensor([5, pages * bs + 3, -1], dtype=torch.int64)
+    caches = make_caches(pages, bs, hk, cache_dtype, seed=13)
+    in_range = slots.clone()
+    in_range[in_range >= pages * bs] = -1
+    expect = oracle_store(k.float() @ Rs[0], v.float() @ Rs[1], caches, in_range, 0.96, 0.92)
+    dev = [c.to(device) for c in caches]
+    ops = [quant.rotation_operand(R.to(device)) for R in Rs]
+    quant.quant_write(k.to(device), v.to(device), ops[0], ops[1], dev[0], dev[1], slots.to(device),
+                      quant.clip_index(0.96, D), quant.clip_index(0.92, D), hk, D)
+    torch.cuda.synchronize()
+    for i, (got, want) in enumerate(zip(dev, expect)):
+        g8, w8 = got.cpu().view(torch.uint8), want.view(torch.uint8)
+        if i == 0:
+            g8, w8 = zero_sign_free(g8), zero_sign_free(w8)
+        assert torch.equal(g8, w8)
