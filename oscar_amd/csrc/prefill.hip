@@ -204,6 +204,12 @@ __device__ __forceinline__ uint32_t magic_pair(uint32_t w, int sh) {
 // a code dword yields a pair; the Q^T operand uses the same order.
 __device__ __forceinline__ int k_feature(int p) { return (p >> 1) + 8 * (p & 1); }
 
+// 16-byte chunk q8 (0..3) of feature group kfg sits at position
+// (q8 + kfg / 2) mod 4 of the group's 64 bytes: the eight threads that write
+// one row store chunk q8 into eight different bank groups at once (unrotated,
+// groups 0, 2, 4, 6 and 1, 3, 5, 7 collided pairwise; measured C4 -3 %).
+__device__ __forceinline__ int k_chunk_slot(int q8, int kfg) { return (q8 + (kfg >> 1)) & 3; }
+
 // A thread's 32 K values (features 32 kfg .. +31, natural order) into its
 // token's row in the permuted order.
 __device__ __forceinline__ void store_k_values(const float (&kv)[32], int ktt, int kfg, _Float16* kh) {
@@ -213,7 +219,7 @@ __device__ __forceinline__ void store_k_values(const float (&kv)[32], int ktt, i
     half8 x;
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = to_h(kv[16 * (q8 >> 1) + k_feature(8 * (q8 & 1) + e)]);
-    dst[q8] = x;
+    dst[k_chunk_slot(q8, kfg)] = x;
   }
 }
 
@@ -259,8 +265,9 @@ __device__ __forceinline__ void store_hist(const PrefillArgs& a, const HistLoad&
       for (int q8 = 0; q8 < 4; ++q8) {
         const uint32_t w = L.k[q8 >> 1];
         const int j0 = 4 * (q8 & 1);
-        dst[q8] = __builtin_bit_cast(half8, u32x4{magic_pair(w, 2 * j0), magic_pair(w, 2 * j0 + 2),
-                                                  magic_pair(w, 2 * j0 + 4), magic_pair(w, 2 * j0 + 6)});
+        dst[k_chunk_slot(q8, kfg)] = __builtin_bit_cast(
+            half8, u32x4{magic_pair(w, 2 * j0), magic_pair(w, 2 * j0 + 2), magic_pair(w, 2 * j0 + 4),
+                         magic_pair(w, 2 * j0 + 6)});
       }
     } else {
       const floatx4* src = reinterpret_cast<const floatx4*>(
@@ -459,6 +466,9 @@ __global__ __launch_bounds__(512, 1) void prefill_kernel(PrefillArgs a) {
   auto hi_wave = [&](bool hist) {
     return wave_full ? (hist ? (int32_t)C - 1 : full_hi_new) : (int32_t)-1;
   };
+  // Offsets (halves) of a K operand chunk for this lane's g: + 8g, or - 24g
+  // where the rotated slot wraps from 3 to 0.
+  const int kstep = 8 * g, kwrap = -24 * g;
   float qsum;
   {
     // Q^T operands of the wave's rows in the K tiles' feature order: lane
@@ -498,12 +508,20 @@ __global__ __launch_bounds__(512, 1) void prefill_kernel(PrefillArgs a) {
     if (k0 < keys_wave) {
       const _Float16* kh = S.kh[i & 1];
       const _Float16* vt = S.vt[i & 1];
+      const _Float16* krow = kh + col * kKs;
       const half8* qsrc = reinterpret_cast<const half8*>(S.q[wave] + (g * kRowsPerWave + col) * 8);
+      // K operand of k-step m: chunk 2m + g of the row (feature group m / 2,
+      // chunk 2 (m % 2) + g), at its rotated slot; the lane's g enters as one
+      // of two per-lane offsets (with or without the wrap of the slot).
+      auto kchunk = [&](int m) {
+        const int c0 = (2 * (m & 1) + (m >> 2)) & 3;          // slot for g = 0
+        return *reinterpret_cast<const half8*>(krow + 8 * (4 * (m >> 1) + c0) + (c0 == 3 ? kwrap : kstep));
+      };
       floatx16 s0 = floatx16{}, s1 = floatx16{};
 #pragma unroll
       for (int m = 0; m < 16; m += 2) {
-        const half8 ka = *reinterpret_cast<const half8*>(kh + col * kKs + 16 * m + 8 * g);
-        const half8 kb2 = *reinterpret_cast<const half8*>(kh + col * kKs + 16 * (m + 1) + 8 * g);
+        const half8 ka = kchunk(m);
+        const half8 kb2 = kchunk(m + 1);
         s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qsrc[m * 2 * kRowsPerWave], s0, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(kb2, qsrc[(m + 1) * 2 * kRowsPerWave], s1, 0, 0, 0);
       }
