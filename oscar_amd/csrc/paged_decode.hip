@@ -395,7 +395,7 @@ __device__ __forceinline__ T pick4(T v0, T v1, T v2, T v3, int i) {
 // pass they are newer than every image load.  The single-step workgroups
 // (long-history MTP reads such as 1 x 4 tokens over 24K) run the first
 // instance, whose allocation was tuned for their window tiles; multi-step
-// launches run the second (C3 55.1 -> 54.0 us, C5 38.5 -> 37.7 us).
+// launches run the second (C3 55.1 -> 54.1 us; C5 unchanged within noise).
 template <bool kMidIssue>
 __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];

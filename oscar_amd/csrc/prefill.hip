@@ -207,7 +207,7 @@ __device__ __forceinline__ int k_feature(int p) { return (p >> 1) + 8 * (p & 1);
 // 16-byte chunk q8 (0..3) of feature group kfg sits at position
 // (q8 + kfg / 2) mod 4 of the group's 64 bytes: the eight threads that write
 // one row store chunk q8 into eight different bank groups at once (unrotated,
-// groups 0, 2, 4, 6 and 1, 3, 5, 7 collided pairwise; measured C4 -3 %).
+// the eight stores fell into two bank groups; measured C4 2.18 -> 2.08 ms).
 __device__ __forceinline__ int k_chunk_slot(int q8, int kfg) { return (q8 + (kfg >> 1)) & 3; }
 
 // A thread's 32 K values (features 32 kfg .. +31, natural order) into its

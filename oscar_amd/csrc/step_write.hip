@@ -12,6 +12,8 @@
 //     sets owner = its page if the window keeps it (position >= seq - recent
 //     or < sink_eff), else -1, and a kept winner stores its unclipped k_rot /
 //     v_rot and their fp16 operand images (window_images.h).
+// oscar_quant_write runs the same kernel without a query or window (num_heads
+// = 0, no arena) for writes of at most 2048 key + value vectors.
 //
 // Work layout: a 1024-thread workgroup rotates up to four vectors that share a
 // rotation (query heads, key heads or value heads of consecutive tokens).
