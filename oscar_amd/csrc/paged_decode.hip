@@ -386,6 +386,23 @@ __device__ __forceinline__ T pick4(T v0, T v1, T v2, T v3, int i) {
   return i == 0 ? v0 : (i == 1 ? v1 : (i == 2 ? v2 : v3));
 }
 
+template <int kCtrl>
+__device__ __forceinline__ float dpp_move(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xF, 0xF, false));
+}
+
+// Max / sum over the 32 lanes of this lane's half wave, in every lane: quad
+// xor 1 and 2, half-row and row mirrors, then the other 16 lanes.
+template <bool kMax>
+__device__ __forceinline__ float half_wave_reduce(float x) {
+  auto op = [](float u, float v) { return kMax ? fmaxf(u, v) : u + v; };
+  x = op(x, dpp_move<0xB1>(x));
+  x = op(x, dpp_move<0x4E>(x));
+  x = op(x, dpp_move<0x141>(x));
+  x = op(x, dpp_move<0x140>(x));
+  return op(x, shfl_xor_f32(x, 16));
+}
+
 // kMidIssue selects where the step loop requests the next step's loads: at
 // the top of the step (false), or after the step's score pass (true), where
 // every image load of the step has been issued before them.  Loads complete
@@ -396,7 +413,13 @@ __device__ __forceinline__ T pick4(T v0, T v1, T v2, T v3, int i) {
 // (long-history MTP reads such as 1 x 4 tokens over 24K) run the first
 // instance, whose allocation was tuned for their window tiles; multi-step
 // launches run the second (C3 55.1 -> 54.1 us; C5 unchanged within noise).
-template <bool kMidIssue>
+// kSmall: every item of the launch has at most 8 rows (single-token requests
+// of a GQA group of 1..8, or two tokens of a group of 4): the score tile is
+// computed as S = Q K^T instead, so a lane holds one token and 16 rows of
+// which only registers 0..3 (rows 4g .. 4g + 3) are real, and the softmax
+// runs on those 4 values per lane (with half-wave reductions over tokens)
+// instead of on 16 mostly padded ones.
+template <bool kMidIssue, bool kSmall>
 __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
   // History splits are dispatched as 0, S - 1, S - 2, ..., 1: the first and
@@ -537,6 +560,12 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   floatx16 acc[2] = {floatx16{}, floatx16{}};   // O^T of features 64w .. 64w + 63 (2 blocks of 32)
   float m_run = -__builtin_inff();
   float l_run = 0.f, z_run = 0.f, ps_run = 0.f;  // this lane's share of its row's sums (own tiles)
+  // kSmall: running maxima and this lane's (token's) shares of the sums of
+  // rows 4g .. 4g + 3, and those rows' q sums.
+  float m4[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+  float l4[4] = {0.f, 0.f, 0.f, 0.f}, z4[4] = {0.f, 0.f, 0.f, 0.f}, ps4[4] = {0.f, 0.f, 0.f, 0.f};
+  floatx4 qs4 = floatx4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (kSmall) qs4 = *reinterpret_cast<const floatx4*>(&S.qsum[4 * g]);
   const float qsum = S.qsum[col];
   const uint32_t ones16 = magic_ones();
   // PV operand lane constants: block b, row m = col is code sp = 2b + (m & 1)
@@ -579,6 +608,9 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
 
     // ---- own tile: token parameters and byte-transposed V codes ----
     bool big;
+    // kSmall: this lane's token's parameters stay in registers
+    float t_a = 0.f, t_b = 0.f, t_m = 0.f, t_vs = 0.f, t_rv = 0.f, t_vz = 0.f;
+    bool t_win = false;
     {
       const bool win = (wmw >> col) & 1u;
       const bool used = col < nvalid && !win;
@@ -586,7 +618,15 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
       const float kz = f16_bits_to_f32(L.meta[0] >> 16);
       const float vsc = f16_bits_to_f32(L.meta[1]);
       const float vz = f16_bits_to_f32(L.meta[1] >> 16);
-      if (g == 0) {
+      if constexpr (kSmall) {
+        t_a = used ? 4.f * ksc * a.scale_log2 : (win ? a.scale_log2 : 0.f);
+        t_b = used ? (kz - 4.f * ksc) * a.scale_log2 : 0.f;
+        t_m = (used || win) ? 0.f : -__builtin_inff();
+        t_rv = used ? 1.f / vsc : 0.f;
+        t_vs = used ? vsc : 0.f;
+        t_vz = used ? vz * t_rv : 0.f;
+        t_win = win;
+      } else if (g == 0) {
         S.ta[w][col] = used ? 4.f * ksc * a.scale_log2 : (win ? a.scale_log2 : 0.f);
         S.tb[w][col] = used ? (kz - 4.f * ksc) * a.scale_log2 : 0.f;
         S.tm[w][col] = (used || win) ? 0.f : -__builtin_inff();
@@ -620,6 +660,15 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
       // One accumulator chain: the other workgroup on the SIMD covers the
       // MFMA latency.
       s = floatx16{};
+      // S^T = K Q^T (lane: row col, 16 tokens), or S = Q K^T in the kSmall
+      // instance (lane: token col, rows 8 (r / 4) + 4g + r % 4): the same
+      // operand registers either way.
+      auto score_mfma = [&](const half8& kop, const half8& qop) {
+        if constexpr (kSmall)
+          s = __builtin_amdgcn_mfma_f32_32x32x16_f16(qop, kop, s, 0, 0, 0);
+        else
+          s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qop, s, 0, 0, 0);
+      };
       half8 qa = qsrc[0], qb = qsrc[2 * kRows], qal = qlsrc[0], qbl = qlsrc[2 * kRows];
       auto qk_pair = [&](int j, const half8& k0, const half8& k1) {
         half8 na = qa, nb = qb, nal = qal, nbl = qbl;
@@ -629,10 +678,10 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
           nal = qlsrc[(2 * j + 2) * 2 * kRows];
           nbl = qlsrc[(2 * j + 3) * 2 * kRows];
         }
-        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qa, s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qb, s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qal, s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qbl, s, 0, 0, 0);
+        score_mfma(k0, qa);
+        score_mfma(k1, qb);
+        score_mfma(k0, qal);
+        score_mfma(k1, qbl);
         qa = na;
         qb = nb;
         qal = nal;
@@ -673,8 +722,8 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
         for (int j = 0; j < 8; ++j) {
           const half8 la = __builtin_bit_cast(half8, im[2 * j]);
           const half8 lb = __builtin_bit_cast(half8, im[2 * j + 1]);
-          s = __builtin_amdgcn_mfma_f32_32x32x16_f16(la, qsrc[(2 * j) * 2 * kRows], s, 0, 0, 0);
-          s = __builtin_amdgcn_mfma_f32_32x32x16_f16(lb, qsrc[(2 * j + 1) * 2 * kRows], s, 0, 0, 0);
+          score_mfma(la, qsrc[(2 * j) * 2 * kRows]);
+          score_mfma(lb, qsrc[(2 * j + 1) * 2 * kRows]);
         }
       }
     }
@@ -698,28 +747,44 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
       }
     }
     issue_next();
-    // scores (lane: row col, tokens 8 (r / 4) + 4g + r % 4) and the tile's row max
-    float mb = -__builtin_inff();
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const floatx4 av = *reinterpret_cast<const floatx4*>(&S.ta[w][8 * jj + 4 * g]);
-      const floatx4 bv = *reinterpret_cast<const floatx4*>(&S.tb[w][8 * jj + 4 * g]);
-      const floatx4 tmv = *reinterpret_cast<const floatx4*>(&S.tm[w][8 * jj + 4 * g]);
+    if constexpr (kSmall) {
+      // scores of rows 4g + i (i < 4) against this lane's token; row maxima
+      // over the tile's 32 tokens (the half wave)
+      floatx4 mb4;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        s[4 * jj + i] = fmaf(av[i], s[4 * jj + i], bv[i] * qsum) + tmv[i];
-        mb = fmaxf(mb, s[4 * jj + i]);
+        s[i] = fmaf(t_a, s[i], t_b * qs4[i]) + t_m;
+        mb4[i] = half_wave_reduce<true>(s[i]);
       }
+      if (col == 0) *reinterpret_cast<floatx4*>(&S.mx[w][4 * g]) = mb4;
+    } else {
+      // scores (lane: row col, tokens 8 (r / 4) + 4g + r % 4) and the tile's row max
+      float mb = -__builtin_inff();
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const floatx4 av = *reinterpret_cast<const floatx4*>(&S.ta[w][8 * jj + 4 * g]);
+        const floatx4 bv = *reinterpret_cast<const floatx4*>(&S.tb[w][8 * jj + 4 * g]);
+        const floatx4 tmv = *reinterpret_cast<const floatx4*>(&S.tm[w][8 * jj + 4 * g]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          s[4 * jj + i] = fmaf(av[i], s[4 * jj + i], bv[i] * qsum) + tmv[i];
+          mb = fmaxf(mb, s[4 * jj + i]);
+        }
+      }
+      mb = fmaxf(mb, shfl_xor_f32(mb, 32));
+      if (g == 0) S.mx[w][col] = mb;
     }
-    mb = fmaxf(mb, shfl_xor_f32(mb, 32));
-    if (g == 0) S.mx[w][col] = mb;
     if (lane == 0) S.big[w] = big ? 1u : 0u;
     lds_barrier();
 
     // ---- common max of the step (same decision in every wave), P' of the own tile ----
+    const bool eager = (S.big[0] | S.big[1] | S.big[2] | S.big[3]) != 0u;
     {
-      const float M = fmaxf(fmaxf(S.mx[0][col], S.mx[1][col]), fmaxf(S.mx[2][col], S.mx[3][col]));
-      const bool eager = (S.big[0] | S.big[1] | S.big[2] | S.big[3]) != 0u;
+      // (kSmall: rows 8 and up of the row maxima are not written; those O^T
+      // columns are never stored)
+      const float M = (kSmall && col >= 8)
+                          ? -__builtin_inff()
+                          : fmaxf(fmaxf(S.mx[0][col], S.mx[1][col]), fmaxf(S.mx[2][col], S.mx[3][col]));
       const bool need = M > m_run + (eager ? 0.f : kLazy);
       const bool resc = need && m_run != -__builtin_inff();
       if (__ballot(resc)) {
@@ -732,7 +797,43 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
       }
       if (need) m_run = M;
     }
-    {
+    if constexpr (kSmall) {
+      // Rows 4g + i: the same decisions on the same maxima, then P' of this
+      // lane's token for each row into its slot of the row (slots 4u + v
+      // hold tokens 4u + (0, 2, 1, 3)[v]), and the token's shares of the
+      // row sums over the weights as the PV pass sees them.
+      floatx4 M4 = *reinterpret_cast<const floatx4*>(&S.mx[0][4 * g]);
+#pragma unroll
+      for (int ww = 1; ww < kWaves; ++ww) {
+        const floatx4 x = *reinterpret_cast<const floatx4*>(&S.mx[ww][4 * g]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) M4[i] = fmaxf(M4[i], x[i]);
+      }
+      const int slot = (col & ~3) | ((col & 1) << 1) | ((col >> 1) & 1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool need = M4[i] > m4[i] + (eager ? 0.f : kLazy);
+        const bool resc = need && m4[i] != -__builtin_inff();
+        const float alpha = resc ? exp2_raw(m4[i] - M4[i]) : 1.f;
+        l4[i] *= alpha;
+        z4[i] *= alpha;
+        ps4[i] *= alpha;
+        if (need) m4[i] = M4[i];
+        const float m_use = m4[i] == -__builtin_inff() ? 0.f : m4[i];
+        const float pr = exp2_raw(s[i] - m_use);
+        const _Float16 h = (_Float16)(pr * t_vs);
+        S.p[w][(4 * g + i) * kPRow + slot] = h;
+        const float wh = (float)h;
+        ps4[i] += wh;
+        l4[i] = fmaf(wh, t_rv, l4[i]);
+        z4[i] = fmaf(wh, t_vz, z4[i]);
+        if (wmw != 0u) {
+          const _Float16 hw = t_win ? (_Float16)(0.25f * pr) : (_Float16)0.f;
+          S.pw[w][(4 * g + i) * kPRow + slot] = hw;
+          l4[i] = fmaf(4.f, (float)hw, l4[i]);
+        }
+      }
+    } else {
       // exp2(-inf - m) = 0 needs a finite m: rows that have seen no key yet use 0.
       const float m_use = m_run == -__builtin_inff() ? 0.f : m_run;
       float psum = 0.f, zsum = 0.f, pss = 0.f;
@@ -839,15 +940,30 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   // ---- row sums over both lane halves and the four waves, then the partial ----
   // The sums go through the Q^T area, which no wave reads after the last
   // step's scores (every wave has passed that step's barriers by now).
-  l_run += shfl_xor_f32(l_run, 32);
-  z_run += shfl_xor_f32(z_run, 32);
-  ps_run += shfl_xor_f32(ps_run, 32);
   float* red = reinterpret_cast<float*>(S.q);
   static_assert(sizeof(S.q) >= kWaves * 3 * kRows * sizeof(float), "row sums fit the Q^T area");
-  if (g == 0) {
-    red[(w * 3 + 0) * kRows + col] = l_run;
-    red[(w * 3 + 1) * kRows + col] = z_run;
-    red[(w * 3 + 2) * kRows + col] = ps_run;
+  if constexpr (kSmall) {
+    // rows 4g + i: sums over the half wave's tokens
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lt = half_wave_reduce<false>(l4[i]);
+      const float zt = half_wave_reduce<false>(z4[i]);
+      const float pt = half_wave_reduce<false>(ps4[i]);
+      if (col == 0) {
+        red[(w * 3 + 0) * kRows + 4 * g + i] = lt;
+        red[(w * 3 + 1) * kRows + 4 * g + i] = zt;
+        red[(w * 3 + 2) * kRows + 4 * g + i] = pt;
+      }
+    }
+  } else {
+    l_run += shfl_xor_f32(l_run, 32);
+    z_run += shfl_xor_f32(z_run, 32);
+    ps_run += shfl_xor_f32(ps_run, 32);
+    if (g == 0) {
+      red[(w * 3 + 0) * kRows + col] = l_run;
+      red[(w * 3 + 1) * kRows + col] = z_run;
+      red[(w * 3 + 2) * kRows + col] = ps_run;
+    }
   }
   lds_barrier();
   float lt = 0.f, zt = 0.f, pt = 0.f;
@@ -1346,28 +1462,36 @@ int fill_common(DecodeArgs& a, const float* q_rot, int32_t num_heads, int32_t nu
   return kOk;
 }
 
-std::atomic<uint64_t> g_split_lds_set[2] = {{0}, {0}};
+std::atomic<uint64_t> g_split_lds_set[3] = {{0}, {0}, {0}};
 
 int set_split_lds() {
-  const int rc = set_dynamic_lds(reinterpret_cast<const void*>(paged_decode_split_kernel<false>), (int)kLdsBytes,
-                                 g_split_lds_set[0]);
-  if (rc != kOk) return rc;
-  return set_dynamic_lds(reinterpret_cast<const void*>(paged_decode_split_kernel<true>), (int)kLdsBytes,
-                         g_split_lds_set[1]);
+  const void* k[3] = {reinterpret_cast<const void*>(paged_decode_split_kernel<false, false>),
+                      reinterpret_cast<const void*>(paged_decode_split_kernel<true, false>),
+                      reinterpret_cast<const void*>(paged_decode_split_kernel<true, true>)};
+  for (int i = 0; i < 3; ++i) {
+    const int rc = set_dynamic_lds(k[i], (int)kLdsBytes, g_split_lds_set[i]);
+    if (rc != kOk) return rc;
+  }
+  return kOk;
 }
 
 // Split kernel instance of a launch chunk: the mid-step load issue when some
-// item has more 128-token steps than there are splits.
+// item has more 128-token steps than there are splits, with the small-row
+// score tile when no item has more than 8 rows.
 void launch_split(const DecodeArgs& a, unsigned nitems, dim3 grid, hipStream_t stream) {
-  bool multi = false;
+  bool multi = false, small = true;
   for (unsigned i = 0; i < nitems; ++i) {
+    if (a.items[i].nq <= 0) continue;
     const int64_t steps = ((int64_t)a.items[i].prefix + kStepTok - 1) / kStepTok;
-    if (a.items[i].nq > 0 && steps > a.max_splits) multi = true;
+    if (steps > a.max_splits) multi = true;
+    if ((int64_t)a.items[i].nq * a.group > 8) small = false;
   }
-  if (multi)
-    hipLaunchKernelGGL(paged_decode_split_kernel<true>, grid, dim3(256), kLdsBytes, stream, a);
+  if (multi && small)
+    hipLaunchKernelGGL((paged_decode_split_kernel<true, true>), grid, dim3(256), kLdsBytes, stream, a);
+  else if (multi)
+    hipLaunchKernelGGL((paged_decode_split_kernel<true, false>), grid, dim3(256), kLdsBytes, stream, a);
   else
-    hipLaunchKernelGGL(paged_decode_split_kernel<false>, grid, dim3(256), kLdsBytes, stream, a);
+    hipLaunchKernelGGL((paged_decode_split_kernel<false, false>), grid, dim3(256), kLdsBytes, stream, a);
 }
 
 // Merge blocks per feature quarter: one per row of a row tile that can hold

@@ -121,3 +121,25 @@ def test_multi_step_splits_with_window(device, bs, tiles_per_split):
     err = (got - want).abs().max().item()
     assert torch.isfinite(got).all()
     assert err <= REL_TOL * want.abs().max().item(), f"max err {err:.3e}"
+
+
+@pytest.mark.parametrize("q_len,hk,hq", [(1, 1, 6), (2, 1, 4), (1, 2, 16), (1, 1, 1)])
+@pytest.mark.parametrize("window", [True, False])
+def test_multi_step_small_row_items(device, q_len, hk, hq, window):
+    """Launches whose items have at most 8 rows (q_len x group) and more
+    128-token steps than splits (48 requests over 1500..4200-token histories)
+    run the small-row score tile: parity with the oracle, window on and off."""
+    g = torch.Generator().manual_seed(100 * q_len + 10 * hk + hq)
+    hist = torch.randint(1500, 4200, (48,), generator=g).tolist()
+    case = decode_case(hist, [q_len] * 48, seed=5 + hq, hk=hk, hq=hq, window=window, pool_pages=48 * 34 + 64,
+                       bs=128)
+    L = case.layer
+    q, k, v = case.rotated()
+    stage = L.stage() if L.window_enabled else None
+    want = oatt.paged_attention_ref(q, k, v, L.k_cache, L.v_cache, case.bt, case.qsl, case.seqs, L.scale, stage)
+    dstage = None if stage is None else tuple(t.to(device) for t in stage)
+    got = decode.paged_attention(q.to(device), k.to(device), v.to(device), L.k_cache.to(device),
+                                 L.v_cache.to(device), case.bt.to(device), case.qsl, case.seqs, L.scale,
+                                 dstage).cpu()
+    assert torch.isfinite(got).all()
+    assert (got - want).abs().max() <= 1e-3 * max(want.abs().max().item(), 1e-6)
