@@ -416,9 +416,11 @@ __device__ __forceinline__ float half_wave_reduce(float x) {
 // kSmall: every item of the launch has at most 8 rows (single-token requests
 // of a GQA group of 1..8, or two tokens of a group of 4): the score tile is
 // computed as S = Q K^T instead, so a lane holds one token and 16 rows of
-// which only registers 0..3 (rows 4g .. 4g + 3) are real, and the softmax
-// runs on those 4 values per lane (with half-wave reductions over tokens)
-// instead of on 16 mostly padded ones.
+// which registers 0..3 (rows 4g .. 4g + 3) are the rows' high-part products
+// and registers 4..7 their low-part products (rows 8 .. 15 of the Q operand
+// hold the low parts, which halves the score MFMAs), and the softmax runs on
+// 4 values per lane (with half-wave reductions over tokens) instead of on 16
+// mostly padded ones.
 template <bool kMidIssue, bool kSmall>
 __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
@@ -654,7 +656,12 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
       // Q^T operands (high and low parts, so the products see q to 2^-22;
       // the code operands 1 + c/4 are exact) are read from LDS one k-step
       // pair ahead of their use.
-      const half8* qsrc = reinterpret_cast<const half8*>(&S.q[(g * kRows + col) * 8]);   // + m * 2 * kRows
+      // kSmall: rows 8 .. 15 of the Q operand are the low parts of rows
+      // 0 .. 7, so one MFMA pass gives both products (row r: high part,
+      // row 8 + r: low part; the fixup adds them).
+      const half8* qsrc = reinterpret_cast<const half8*>(
+          (kSmall && (col & 24) == 8) ? &S.qlo[(g * kRows + col - 8) * 8]
+                                      : &S.q[(g * kRows + col) * 8]);   // + m * 2 * kRows
       const half8* qlsrc = reinterpret_cast<const half8*>(&S.qlo[(g * kRows + col) * 8]);
       const uint32_t kw[8] = {L.kc0[0], L.kc0[1], L.kc0[2], L.kc0[3], L.kc1[0], L.kc1[1], L.kc1[2], L.kc1[3]};
       // One accumulator chain: the other workgroup on the SIMD covers the
@@ -669,19 +676,27 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
         else
           s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qop, s, 0, 0, 0);
       };
-      half8 qa = qsrc[0], qb = qsrc[2 * kRows], qal = qlsrc[0], qbl = qlsrc[2 * kRows];
+      half8 qa = qsrc[0], qb = qsrc[2 * kRows], qal{}, qbl{};
+      if constexpr (!kSmall) {
+        qal = qlsrc[0];
+        qbl = qlsrc[2 * kRows];
+      }
       auto qk_pair = [&](int j, const half8& k0, const half8& k1) {
         half8 na = qa, nb = qb, nal = qal, nbl = qbl;
         if (j < 7) {
           na = qsrc[(2 * j + 2) * 2 * kRows];
           nb = qsrc[(2 * j + 3) * 2 * kRows];
-          nal = qlsrc[(2 * j + 2) * 2 * kRows];
-          nbl = qlsrc[(2 * j + 3) * 2 * kRows];
+          if constexpr (!kSmall) {
+            nal = qlsrc[(2 * j + 2) * 2 * kRows];
+            nbl = qlsrc[(2 * j + 3) * 2 * kRows];
+          }
         }
         score_mfma(k0, qa);
         score_mfma(k1, qb);
-        score_mfma(k0, qal);
-        score_mfma(k1, qbl);
+        if constexpr (!kSmall) {
+          score_mfma(k0, qal);
+          score_mfma(k1, qbl);
+        }
         qa = na;
         qb = nb;
         qal = nal;
@@ -717,7 +732,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
         }
         // window tokens (the other lanes hold zeros): low part of k against
         // the high part of q (the low-low product is below 2^-22 of the
-        // score's terms)
+        // score's terms; kSmall rows 8 .. 15 take it, harmlessly)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const half8 la = __builtin_bit_cast(half8, im[2 * j]);
@@ -753,7 +768,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
       floatx4 mb4;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        s[i] = fmaf(t_a, s[i], t_b * qs4[i]) + t_m;
+        s[i] = fmaf(t_a, s[i] + s[4 + i], t_b * qs4[i]) + t_m;
         mb4[i] = half_wave_reduce<true>(s[i]);
       }
       if (col == 0) *reinterpret_cast<floatx4*>(&S.mx[w][4 * g]) = mb4;
