@@ -159,7 +159,13 @@ int oscar_paged_decode_rotated(const float* q_rot, const float* k_new, const flo
  * entry allocates nothing and needs no zeroed memory.  Calls that overlap on
  * one GPU (several streams) share the array and race; the array keeps the
  * last call's partials.  Arguments as oscar_paged_decode.
+ * Under graph capture: query_start_loc and seq_lens are read from host
+ * memory when the call is made and placed in the kernel arguments, so a
+ * captured launch replays the captured step's request layout on every
+ * replay; only steps of a fixed layout (same query starts and lengths)
+ * replay correctly.
  */
+#define OSCAR_DECODE_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20) /* the device array's size, per GPU */
 int oscar_paged_decode_noalloc(const float* q_rot, const float* k_new, const float* v_new,
                                int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
                                int32_t head_size, const void* k_cache, const void* v_cache,

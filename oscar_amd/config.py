@@ -16,11 +16,15 @@ Variables (an unset, empty or unparsable numeric value means its default):
   OSCAR_ASCEND_STAGING_TOKENS    int    8192  negative counts as 0
   OSCAR_ASCEND_GROUP_SIZE        int    0     anything else is rejected
   OSCAR_ASCEND_VERBOSE           flag   on    "0" turns it off
-  OSCAR_ASCEND_USE_PAGED         flag   on    "0": every request takes the
-                                              prefill-continuation kernel
+  OSCAR_ASCEND_USE_PAGED         switch on    when set, only "1" turns it on
+                                              (as the reference reads it); any
+                                              other value: every request takes
+                                              the prefill-continuation kernel
 
-USE_PAGED defaults to on here (the reference defaults it off until its NPU
-kernel was probed): short requests then take the paged HIP decode kernel.
+USE_PAGED defaults to on here when the variable is unset (the reference
+defaults it off until its NPU kernel was probed): short requests then take
+the paged HIP decode kernel.  A set value is read as the reference reads it,
+so OSCAR_ASCEND_USE_PAGED=0, =false or =off all turn the paged route off.
 OSCAR_ASCEND_USE_TRITON, OSCAR_ASCEND_FUSED_PREP and OSCAR_ASCEND_ENABLE
 select between the reference's own kernel variants; they are accepted and
 have no effect, as there is a single HIP path.
@@ -53,8 +57,15 @@ def _count(env: Mapping[str, str], name: str, default: int) -> int:
 
 
 def _flag(env: Mapping[str, str], name: str, default: bool) -> bool:
+    """On unless set to "0" (config.py:90, VERBOSE)."""
     text = env.get(PREFIX + name)
     return default if text is None else text != "0"
+
+
+def _switch(env: Mapping[str, str], name: str, default: bool) -> bool:
+    """Off unless set to "1" (config.py:93, USE_PAGED); `default` when unset."""
+    text = env.get(PREFIX + name)
+    return default if text is None else text == "1"
 
 
 @dataclass(frozen=True)
@@ -109,6 +120,6 @@ class OscarConfig:
             sink_tokens=_count(env, "SINK_TOKENS", 64),
             recent_tokens=_count(env, "RECENT_TOKENS", 256),
             staging_tokens=_count(env, "STAGING_TOKENS", 8192),
-            use_paged=_flag(env, "USE_PAGED", True),
+            use_paged=_switch(env, "USE_PAGED", True),
             verbose=_flag(env, "VERBOSE", True),
         )

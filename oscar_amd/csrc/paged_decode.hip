@@ -1693,7 +1693,7 @@ int paged_decode(const float* q_rot, const float* k_new, const float* v_new, int
 // Device scratch of the no-allocation entry (oscar_paged_decode_noalloc):
 // the split partials of one launch, at most kScratchBytes.  Every GPU the
 // library runs on holds its own copy until the process ends.
-constexpr size_t kScratchBytes = size_t(32) << 20;
+constexpr size_t kScratchBytes = OSCAR_DECODE_NOALLOC_SCRATCH_BYTES;
 
 }  // namespace
 }  // namespace oscar

@@ -9,7 +9,9 @@ whole cache blocks.  Per OSCAR layer the fixed buffers here are
   * its fp16 MFMA operand images (K high and   rows * bs * 3 * Hk * D * 2
     low parts, V)
   * the arena's seat-winner scratch            rows * bs * 4
-and, once per device, the split-decode workspace of the largest batch.
+and, once per device, the split-decode workspace of the largest batch and
+the library's no-allocation decode array (32 MiB, a static device array every
+GPU that loads the library holds whether or not that entry is called).
 
 The engine seams (``install_runner_hooks``) apply that budget before vLLM
 allocates its caches and print one READY manifest per rank after it did;
@@ -24,6 +26,7 @@ from pathlib import Path
 
 MI355X_HBM_BYTES = 288 * 10 ** 9
 ROTATION_OPERAND_BYTES = 524288        # oscar_rotation_operand_bytes(256): MFMA tiles + fp32 R
+NOALLOC_SCRATCH_BYTES = 32 << 20       # OSCAR_DECODE_NOALLOC_SCRATCH_BYTES: resident once per device
 
 
 def memory_budget(available: int, native_per_block: int, shadow_per_block: int, fixed_bytes: int) -> int:
@@ -102,6 +105,7 @@ def plan_capacity(available: int, layers: int, head_dim: int = 256, num_kv_heads
     """Budget one GPU: how many cache blocks (and INT2 tokens) fit."""
     fixed = layers * fixed_bytes_per_layer(head_dim, num_kv_heads, block_size, sink, recent, staging, window)
     fixed += decode_workspace_bytes(max_requests, num_kv_heads, num_heads, max_query_len, max_history)
+    fixed += NOALLOC_SCRATCH_BYTES
     native = kv_block_bytes(block_size, num_kv_heads, slot_width, layers)
     budget = memory_budget(available, native, 0, fixed)
     blocks = budget // native
@@ -147,7 +151,8 @@ def _oscar_modules(ctx: dict) -> dict:
 def oscar_fixed_bytes(runner, specs: dict, targets: dict) -> int:
     """Persistent bytes the OSCAR layers allocate after profiling (rotations,
     MFMA operands, window arena and its images, at the engine page size),
-    plus the split-decode workspace of the largest batch, once per device."""
+    plus, once per device, the split-decode workspace of the largest batch
+    and the library's 32 MiB no-allocation decode array."""
     fixed = 0
     hk = heads = 1
     for name, module in targets.items():
@@ -164,6 +169,8 @@ def oscar_fixed_bytes(runner, specs: dict, targets: dict) -> int:
     max_q = 1 + int(getattr(spec_cfg, "num_speculative_tokens", 0) or 0) if spec_cfg is not None else 1
     if targets and max_len > 0:
         fixed += decode_workspace_bytes(max_reqs, hk, heads, max_q, max_len)
+    if targets:
+        fixed += NOALLOC_SCRATCH_BYTES
     return fixed
 
 

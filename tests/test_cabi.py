@@ -114,3 +114,22 @@ def test_struct_layouts_match_the_header(tmp_path):
             if decl:
                 names += [re.sub(r"^.*[\s*]", "", part.strip()) for part in decl.split(",")]
         assert names == [f for f, _ in cls._fields_], cname
+
+
+def test_noalloc_scratch_size_is_budgeted(tmp_path):
+    """The no-allocation decode's device array (resident on every GPU that
+    loads the library) is the size the memory plan reserves per device."""
+    from oscar_amd import integration
+
+    src = tmp_path / "scratch.c"
+    src.write_text('#include <stdio.h>\n#include "oscar_amd.h"\n'
+                   'int main(void) { printf("%zu\\n", OSCAR_DECODE_NOALLOC_SCRATCH_BYTES); return 0; }\n')
+    exe = tmp_path / "scratch"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", str(HEADER.parent), str(src), "-o", str(exe)],
+                   check=True, capture_output=True, text=True)
+    size = int(subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout)
+    assert size == integration.NOALLOC_SCRATCH_BYTES == 32 << 20
+    plan = integration.plan_capacity(integration.MI355X_HBM_BYTES - 20 * 10 ** 9, layers=16)
+    bare = (16 * integration.fixed_bytes_per_layer(256, 1, 128, 128, 256, 8192, True)
+            + integration.decode_workspace_bytes(256, 1, 6, 4, 262144))
+    assert plan["fixed"] == bare + size

@@ -49,6 +49,22 @@ def test_config_env_keys(clean_env):
     assert (cfg.k_clip_ratio, cfg.v_clip_ratio) == (0.96, 0.92)
     assert cfg.sink_tokens == 0 and cfg.staging_tokens == 8192
     assert not cfg.window_enabled and not cfg.use_paged
+
+
+@pytest.mark.parametrize("value, on", [("1", True), ("0", False), ("false", False), ("off", False),
+                                       ("no", False), ("true", False), ("", False), (None, True)])
+def test_config_use_paged_as_the_reference_reads_it(clean_env, value, on):
+    # config.py:93: a set OSCAR_ASCEND_USE_PAGED is on only for "1"; unset
+    # keeps this build's default (on).  VERBOSE stays on unless "0" (:90).
+    if value is not None:
+        clean_env.setenv("OSCAR_ASCEND_USE_PAGED", value)
+        clean_env.setenv("OSCAR_ASCEND_VERBOSE", value)
+    cfg = OscarConfig.from_env(256)
+    assert cfg.use_paged is on
+    assert cfg.verbose is (value != "0")
+
+
+def test_config_rejections(clean_env):
     clean_env.setenv("OSCAR_ASCEND_K_CLIP_RATIO", "1.5")
     with pytest.raises(ValueError):
         OscarConfig.from_env(256)

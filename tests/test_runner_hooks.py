@@ -34,7 +34,7 @@ def start(engine, monkeypatch):
 def expected_fixed(engine, num_layers=1, hk=1, heads=6, window=True):
     per_layer = integration.fixed_bytes_per_layer(HEAD, hk, engine.block_size, 64, 64, 256, window)
     workspace = integration.decode_workspace_bytes(4, hk, heads, 4, 4096)
-    return num_layers * per_layer + workspace
+    return num_layers * per_layer + workspace + integration.NOALLOC_SCRATCH_BYTES
 
 
 def test_hooks_budget_then_initialize_and_report(monkeypatch, capsys, no_operand_kernel):
