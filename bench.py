@@ -6,12 +6,15 @@ window) in microseconds per layer and achieved HBM GB/s, plus the
 quantize-write GB/s of a 65,536-token bulk write (random slots, ~1/16
 skipped).
 
-A step is one layer's decode attention (`oscar_paged_decode`: split + merge
-kernels).  Steps cycle through `--layers` distinct per-layer caches (64 x ~13
-MB, beyond the 256 MB Infinity Cache) so reads come from HBM.  Exactly
+A step is one pass of the decode attention (`oscar_paged_decode`: split +
+merge kernels) over all `--layers` distinct per-layer states (64 x ~13 MB,
+beyond the 256 MB Infinity Cache), one call per layer, so every timed step
+reads every layer's history from HBM whatever `--steps` is.  Exactly
 `--warmup` steps are replayed from one HIP graph, then exactly `--steps`
 steps from another, bracketed by device synchronisations and HIP events on
-the replay stream.  Inputs are resident in HBM before timing starts.
+the replay stream; `value` is µs per layer (a step's time / layers) and
+`ms_per_step` the time of one pass.  Inputs are resident in HBM before
+timing starts.
 
 Also in the line (config):
 * forward: the whole impl forward of the same MTP step per layer (fused step
@@ -208,19 +211,21 @@ def decode_only_bytes(st: LayerState) -> dict:
 
 
 def graph_us(calls: list, steps: int, warmup: int) -> float:
-    """Mean µs per call of exactly `steps` calls (cycling through `calls`),
-    replayed from one HIP graph after `warmup` calls replayed from another."""
+    """Mean µs per call over exactly `steps` passes through all of `calls`
+    (one call each, in order), replayed from one HIP graph after `warmup`
+    passes replayed from another."""
     import torch
 
     for c in calls:          # first-call setup (operands, arenas) stays out of the graphs
         c()
     torch.cuda.synchronize()
 
-    def capture(count):
+    def capture(passes):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            for i in range(count):
-                calls[i % len(calls)]()
+            for _ in range(passes):
+                for c in calls:
+                    c()
         return g
 
     warm = capture(warmup) if warmup > 0 else None
@@ -234,7 +239,7 @@ def graph_us(calls: list, steps: int, warmup: int) -> float:
     timed.replay()
     e1.record(stream)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1000.0 / steps
+    return e0.elapsed_time(e1) * 1000.0 / (steps * len(calls))
 
 
 def layer_states(dev, history, q_len, pool, layers, seed=93, window=True):
@@ -291,14 +296,15 @@ def bench_forward(dev, states, steps, warmup):
         c()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(steps):
-        calls[i % len(calls)]()
+    for _ in range(steps):
+        for c in calls:
+            c()
     torch.cuda.synchronize()
-    eager = (time.perf_counter() - t0) * 1e6 / steps
+    eager = (time.perf_counter() - t0) * 1e6 / (steps * len(calls))
     return {"us": us, "eager_us": eager, "out0": out0}
 
 
-def bench_quant_write(dev, steps=64):
+def bench_quant_write(dev, steps=16):
     import torch
 
     from oscar_amd import synthetic
@@ -364,6 +370,34 @@ def bench_prefill(dev, reps=10, seed=71):
     flops = 4 * D * HQ * visible
     return {"us": us, "flops": flops, "tflops": flops / (us * 1e-6) / 1e12, "state": st, "out0": res["out"],
             "steps": reps}
+
+
+def bench_prefill_forward(st: LayerState, reps=5):
+    """The impl forward of the 15360 + 9256 continuation step on the written
+    state: the INT2 write of the 9256 new tokens (rotation on MFMA, clip,
+    quantize, slot write), the window write, the fp32 q/k/v rotations, the
+    prefill kernel, the output rotation and the bf16 cast.  The step's tokens
+    are rewritten with the same values on every call, so the state does not
+    change.  Eager calls (the forward refuses graph capture of a step this
+    size), timed with HIP events on the launch stream."""
+    import torch
+
+    s = st.step
+    out = torch.empty(s.q.shape[0], HQ * D, dtype=torch.bfloat16, device=s.q.device)
+
+    def call():
+        st.impl.forward(st.layer, s.q, s.k, s.v, st.caches, s.md, output=out)
+
+    call()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        call()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return {"us": e0.elapsed_time(e1) * 1000.0 / reps, "steps": reps, "out0": out.clone()}
 
 
 def copy_probe(dev, mib: int) -> None:
@@ -507,9 +541,14 @@ def cpu_read_baseline(st: LayerState, gpu_out, seconds: float, decode_only=False
     want = once()
     rel = (gpu_out.cpu() - want).abs().max().item() / max(want.abs().max().item(), 1e-30)
     med, n = timed_median(once, seconds, min_runs=3)
+    torch.set_num_threads(2)
+    med2, n2 = timed_median(once, seconds, min_runs=3)
+    torch.set_num_threads(cores)
     return {"value": round(med * 1e6, 1), "unit": "us/layer", "cores": cores, "kind": "port",
+            "value_2_threads": round(med2 * 1e6, 1),
             "sample": f"median of {n} runs of the oracle {'DecodeOnly' if decode_only else 'paged MTP'} read "
-                      f"on the same GPU-written state, fp32"}, rel
+                      f"on the same GPU-written state, fp32; the same at 2 threads ({n2} runs) in "
+                      f"value_2_threads"}, rel
 
 
 def cpu_prefill_baseline(st: LayerState, gpu_out, seconds: float):
@@ -532,11 +571,15 @@ def cpu_prefill_baseline(st: LayerState, gpu_out, seconds: float):
                                                L.stage())
 
     med, n = timed_median(once, seconds, min_runs=2)
+    torch.set_num_threads(2)
+    med2, n2 = timed_median(once, seconds, min_runs=2)
+    torch.set_num_threads(cores)
     got, want = gpu_out.cpu(), res["want"]
     ok = bool(((got - want).abs() <= BF16_ABS + BF16_REL * want.abs()).all())
     return {"value": round(med * 1e3, 1), "unit": "ms/layer", "cores": cores, "kind": "port",
-            "sample": f"median of {n} runs of the oracle dense read of the 15360 + 9256 state, fp32"}, ok, \
-        (got - want).abs().max().item()
+            "value_2_threads": round(med2 * 1e3, 1),
+            "sample": f"median of {n} runs of the oracle dense read of the 15360 + 9256 state, fp32; the same "
+                      f"at 2 threads ({n2} runs) in value_2_threads"}, ok, (got - want).abs().max().item(), want
 
 
 # ---------------------------------------------------------------- suite
@@ -566,7 +609,7 @@ SUITE = {
 }
 
 
-def suite(dev, names, cpu_seconds, steps=64):
+def suite(dev, names, cpu_seconds, steps=8):
     out = {}
     long_states = None
     for name in names:
@@ -574,11 +617,22 @@ def suite(dev, names, cpu_seconds, steps=64):
         log(f"bench: suite {name}")
         if name == "C4":
             r = bench_prefill(dev)
-            cpu, ok, err = cpu_prefill_baseline(r["state"], r["out0"], cpu_seconds)
+            cpu, ok, err, want = cpu_prefill_baseline(r["state"], r["out0"], cpu_seconds)
             if not ok:
                 raise SystemExit(f"C4 parity gate failed: max abs err {err:.3e}")
+            fw = bench_prefill_forward(r["state"])
+            want_fwd = (want @ r["state"].layer._oscar_rots[1].cpu().t()).reshape(fw["out0"].shape)
+            got_fwd = fw["out0"].cpu().float()
+            fwd_err = (got_fwd - want_fwd).abs().max().item()
+            if not bool(((got_fwd - want_fwd).abs() <= BF16_ABS + BF16_REL * want_fwd.abs()).all()):
+                raise SystemExit(f"C4 forward parity gate failed: max abs err {fwd_err:.3e}")
             out[name] = {"workload": cfg["workload"], "value": round(r["us"], 2), "unit": "us/layer",
                          "steps": r["steps"],
+                         "forward_us": round(fw["us"], 1), "forward_steps": fw["steps"],
+                         "forward": "the impl forward of the step (INT2 write of the 9256 new tokens with the "
+                                    "MFMA rotation and clip, window write, fp32 q/k/v rotations, the prefill "
+                                    "kernel, output rotation and bf16 cast), eager, HIP events",
+                         "forward_parity_max_abs_err": fwd_err,
                          "arith": "bf16 contract: INT2 codes as exact f16 operands, f16 MFMA, f32 softmax",
                          "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1),
                                       "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
@@ -592,12 +646,12 @@ def suite(dev, names, cpu_seconds, steps=64):
             states = layer_states(dev, suite_histories(name), cfg["q_len"], cfg["pool"], cfg["layers"])
             if name.startswith("C5"):
                 long_states = states
-        dec = bench_decode(dev, states, steps, 16, decode_only=only)
+        dec = bench_decode(dev, states, steps, 2, decode_only=only)
         cpu, rel = cpu_read_baseline(states[0], dec["out0"], cpu_seconds, decode_only=only)
         if not rel <= 1e-3:
             raise SystemExit(f"{name} parity gate failed: rel err {rel:.3e}")
         out[name] = {"workload": cfg["workload"], "value": round(dec["us"], 3), "unit": "us/layer",
-                     "steps": steps,
+                     "steps": steps, "layers_per_step": len(states), "calls_timed": steps * len(states),
                      "roofline": {"bound": "hbm", "achieved": round(dec["gbps"], 1), "peak": HBM_PEAK_GBPS,
                                   "unit": "GB/s", "frac": round(dec["gbps"] / HBM_PEAK_GBPS, 4),
                                   "bytes_per_layer": dec["bytes"]["total"]},
@@ -608,8 +662,8 @@ def suite(dev, names, cpu_seconds, steps=64):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=640)
-    ap.add_argument("--warmup", type=int, default=128)
+    ap.add_argument("--steps", type=int, default=10, help="timed passes over all layer states")
+    ap.add_argument("--warmup", type=int, default=2, help="untimed passes before them")
     ap.add_argument("--layers", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--suite-cpu-seconds", type=float, default=4.0)
@@ -666,7 +720,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": dec["us"] / 1000.0,
+        "ms_per_step": dec["us"] * args.layers / 1000.0,
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -676,6 +730,10 @@ def main():
             "workload": "C2: MTP decode, 1 request x 4 query tokens, Hq=6 Hk=1 D=256, 24579-token INT2 history in "
                         "193 shuffled 128-token pages, FP32 sink=128/recent=256 window (staging 8192), clip "
                         f"0.96/0.92, int8-geometry caches, {args.layers} distinct layers",
+            "step": f"one decode call on each of the {args.layers} distinct layer states; value = a step's "
+                    f"time / {args.layers}",
+            "layers_per_step": args.layers,
+            "calls_timed": args.steps * args.layers,
             "arith": "INT2 codes as exact f16 operands, f16 MFMA with f32 accumulation, f32 online softmax",
             "decode_hbm_gbps": round(dec["gbps"], 1),
             "decode_bytes_per_layer": dec["bytes"]["total"],
@@ -687,13 +745,15 @@ def main():
                             "INT2 write and window write of the 4 new tokens), decode, merge with R_v^T and the "
                             "bf16 cast; bf16 in and out",
                 "us_per_layer": round(fwd["us"], 3), "steps": args.steps, "warmup": args.warmup,
+                "calls_timed": args.steps * args.layers,
                 "eager_us_per_layer": round(fwd["eager_us"], 3),
                 "eager": "the same forwards launched one by one from Python without a graph, wall clock "
                          "over the steps (host work included)",
                 "parity_max_abs_err_vs_oracle": fwd_err},
             "quant_write": None if qw is None else {
                 "workload": "C5 write: 65536 tokens bf16, Hk=1, random slots ~1/16 skipped, rotation on MFMA, "
-                            "clip 0.96/0.92", "steps": qw["steps"],
+                            "clip 0.96/0.92", "steps": qw["steps"], "calls_timed": qw["steps"] * 4,
+                "states": "4 distinct inputs and caches (4 x ~55 MB), one call each per step",
                 "us_per_call": round(qw["us"], 3), "gbps": round(qw["gbps"], 1),
                 "frac_of_hbm_peak": round(qw["gbps"] / HBM_PEAK_GBPS, 4), "bytes_per_call": qw["bytes"],
                 "short_write_us": qw["short_us"],
