@@ -58,6 +58,8 @@
 // head is the sink length when every seat of the sink pages holds its page,
 // else 0; cut starts the run of staged positions that ends at seq - 1 inside
 // [max(seq - recent, head), seq).
+#include <type_traits>
+
 #include "oscar_common.h"
 #include "window_images.h"
 #include "../../include/oscar_amd.h"
@@ -1018,6 +1020,545 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   }
 }
 
+// ---------------------------------------------------------------- small-row split kernel
+// Launches whose items all have at most 8 rows (single-token requests of a
+// GQA group of up to 8: long-context decode, the DecodeOnly read).  Same work
+// split, partials and window semantics as paged_decode_split_kernel, but each
+// wavefront walks its own 32-token tiles (tile w of each of the workgroup's
+// steps) on its own: running maxima and sums per wavefront, no barrier
+// between the wavefronts until the workgroup combines their four partial
+// rows at the end.  A tile's bytes (K codes, meta, V codes, owner tags) are
+// copied straight into a 3-slot LDS ring of the wavefront by buffer loads to
+// LDS, two tiles ahead of the one being computed, so that the history
+// streams without holding registers for the loads in flight.
+//
+// Lane l = (c, G), c = l % 16, G = l / 16, on v_mfma_f32_16x16x32_f16:
+//  * S^T = K Q^T for each half h of the tile: A = K (16 tokens x 32
+//    features): lane (t, G) holds token 8 (t / 4) + 4h + t % 4; B = Q^T:
+//    column c < 8 is the fp16 high part of row c, column 8 + r the low part
+//    of row r, so one pass gives both products and a row-rotation by 8 lanes
+//    adds them.  The result registers r of lane (c, G) are then the scores of
+//    tokens 8G + 4h + r for row c % 8: lane group G holds tokens 8G .. 8G + 7.
+//    K-step s of lane group G covers the features of window-image block
+//    m = 8 (G >> 1) + s, half g = G & 1 (one 16-byte code chunk per half).
+//  * O^T += V^T P'^T over 16 feature tiles n = (q, b, mh): A = V^T: lane
+//    (c, G) holds feature 64q + 32mh + 4 (c >> 1) + 2b + (c & 1) of tokens
+//    8G + {0, 2, 1, 3, 4, 6, 5, 7} (exactly a window V-image chunk), B = P'^T
+//    in the same token order, built from the lane's own scores.  Output lane
+//    (c, G): features 64q + 32mh + 8G + {0, 1, 4, 5} + 2b of row c.
+constexpr int kSmRows = 8;
+constexpr int kSmVtRow = 10;     // dwords per V code byte row: 8 groups of 4 tokens + pad
+constexpr int kSmRing = 3;       // tiles resident per wavefront: the one computed and two in flight
+
+// One tile's bytes as the buffer loads leave them (lane order of each load).
+struct SmallSlot {
+  u32x4 kc[2][64];               // K code chunk of lane l for half h (see load_small_tile)
+  uint8_t vc[kTile][kCodeBytes]; // V code bytes, token-major
+  u32x2 meta[kTile];             // K scale, K zero, V scale, V zero
+  u32x2 own[kTile];              // owner tag (int64) of the token's arena seat
+};
+
+struct SmallTileLds {
+  uint32_t vt[64 * kSmVtRow];    // vt[b * kSmVtRow + t / 4]: byte b of tokens t .. t + 3
+  float prm[6][kTile];           // per token: ta, tb, tm, vs, 1 / vs, vz / vs
+};
+
+struct SmallLds {
+  half8 qt[8][64];               // Q^T operand of k-step s, lane l (shared by the wavefronts)
+  float qs[kWaves][kSmRows];     // the wavefronts' shares of each row's q sum
+  SmallTileLds tile[kWaves];
+  uint32_t wbits[kWaves][kMaxTilesPerSplit / kWaves];   // window-token bits of each of the wavefront's tiles
+  SmallSlot ring[kWaves][kSmRing];
+};
+
+struct SmallCombineLds {
+  float o[kWaves][kSmRows][kHeadDim];
+  float m[kWaves][kSmRows];
+  float l[kWaves][kSmRows];
+};
+
+constexpr size_t kSmallLdsBytes = sizeof(SmallCombineLds) > sizeof(SmallLds)
+                                      ? (sizeof(SmallCombineLds) > sizeof(FreshLds) ? sizeof(SmallCombineLds)
+                                                                                    : sizeof(FreshLds))
+                                      : (sizeof(SmallLds) > sizeof(FreshLds) ? sizeof(SmallLds) : sizeof(FreshLds));
+static_assert(kSmallLdsBytes <= 80 * 1024, "two workgroups' LDS must fit the CU's 160 KiB");
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt vmcnt(n), expcnt and lgkmcnt left at their maxima (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+constexpr int kSmallLoadsPerTile = 6;
+
+// Copy one tile's bytes into a ring slot with six buffer loads to LDS per
+// lane (each lane's 16 or 4 bytes land at slot offset + lane * size).  Every
+// lane issues them whatever the tile holds (an invalid tile reads page 0,
+// positions past the history read the tile's first row; without an arena the
+// owner loads read nothing and leave zeros), so each wait counts exactly
+// whole tiles.  Buffer loads count only in vmcnt.
+__device__ __forceinline__ void load_small_tile(const DecodeArgs& a, SmallSlot& slot, int page, int p0, int prefix,
+                                                int kvh, int lane) {
+  const int c = lane & 15, G = lane >> 4;
+  const bool tile_ok = p0 < prefix && page >= 0;
+  const int pgc = tile_ok ? page : 0;
+  const int prow0 = (int)fast_mod((uint32_t)p0, a.bs_div);
+  const int nrow = tile_ok ? min(kTile, prefix - p0) : 0;       // rows of the tile inside the history
+  auto row_of = [&](int t) { return t < nrow ? prow0 + t : 0; };
+  // Records end at the last code byte of the page's last row of this kv head.
+  const uint32_t krec = (uint32_t)((int64_t)(a.block_size - 1) * a.k_tok + kKCodeOff + kCodeBytes);
+  const uint32_t vrec = (uint32_t)((int64_t)(a.block_size - 1) * a.v_tok + kCodeBytes);
+  const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.k_cache + (int64_t)pgc * a.k_page + (int64_t)kvh * a.k_head), (short)0, krec, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.v_cache + (int64_t)pgc * a.v_page + (int64_t)kvh * a.v_head), (short)0, vrec, 0x00020000);
+  const int kofs = kKCodeOff + 32 * (G & 1) + 16 * (G >> 1);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int tk = 8 * (c >> 2) + 4 * h + (c & 3);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void*)&slot.kc[h][0], 16, row_of(tk) * (int)a.k_tok + kofs,
+                                             0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int tk = 16 * i + (lane >> 2);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_void*)&slot.vc[16 * i][0], 16,
+                                             row_of(tk) * (int)a.v_tok + 16 * (lane & 3), 0, 0, 0);
+  }
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void*)&slot.meta[0], 4,
+                                           row_of(lane >> 1) * (int)a.k_tok + 4 * (lane & 1), 0, 0, 0);
+  // owner tags of the tile's seats (page % rows, prow0 .. prow0 + 31); no arena: zero records
+  const bool arena = a.stage_rows > 0;
+  const int64_t seat0 = arena ? (int64_t)fast_mod((uint32_t)pgc, a.rows_div) * a.block_size + prow0 : 0;
+  const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc(
+      arena ? (void*)(a.owner + seat0) : (void*)a.k_cache, (short)0, arena ? (uint32_t)(kTile * 8) : 0u,
+      0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(orr, (lds_void*)&slot.own[0], 4, 4 * lane, 0, 0, 0);
+}
+
+// x op x^16 and x op x^32 in every lane (gfx950 permlane swaps).
+template <bool kMax>
+__device__ __forceinline__ float across_groups(float x) {
+  auto op = [](float u, float v) { return kMax ? fmaxf(u, v) : u + v; };
+  const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
+  x = op(__int_as_float(s16[0]), __int_as_float(s16[1]));
+  const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return op(__int_as_float(s32[0]), __int_as_float(s32[1]));
+}
+
+__device__ __forceinline__ float ror8_add(float x) {
+  return x + dpp_move<0x128>(x);          // row_ror:8: lane c takes lane (c + 8) % 16 of its row
+}
+
+__global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(DecodeArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
+  const int bx = blockIdx.x;
+  const int item = blockIdx.y;
+  const ItemInfo it = a.items[item];
+  const int rows = it.nq * a.group;
+  if (it.nq <= 0 || blockIdx.z != 0) return;
+  if (a.fresh_block && bx == a.max_splits) {
+    fresh_partial(a, it, item, 0, *reinterpret_cast<FreshLds*>(smem_raw), (int)threadIdx.x);
+    return;
+  }
+  // history splits dispatched as 0, S - 1, S - 2, ..., 1 (the window steps first)
+  const int split = bx == 0 ? 0 : a.max_splits - bx;
+  const int prefix = it.prefix;
+  const int steps = (prefix + kStepTok - 1) / kStepTok;
+  const int rem = a.max_splits > 0 ? steps % a.max_splits : 0;
+  const int fresh_split = steps < a.max_splits ? steps : (rem != 0 ? a.max_splits - 1 : a.max_splits / 2);
+  const bool fresh_here = a.fresh && !a.fresh_block && split == fresh_split;
+  if (split >= steps) {
+    if (fresh_here) fresh_partial(a, it, item, 0, *reinterpret_cast<FreshLds*>(smem_raw), (int)threadIdx.x);
+    return;
+  }
+  SmallLds& S = *reinterpret_cast<SmallLds*>(smem_raw);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15, G = lane >> 4, t32 = lane & 31;
+  const int kvh = it.kvh;
+  const int nsplit = a.max_splits;
+  const int nst = (steps - 1 - split) / nsplit + 1;
+  const bool arena = a.stage_rows > 0;
+  int win_head = 0, win_tail = 0;
+  if (a.win) {
+    typedef __attribute__((address_space(4))) const int32_t const_i32;
+    const const_i32* wb = (const const_i32*)a.win;
+    win_head = wb[2 * it.req];
+    win_tail = wb[2 * it.req + 1];
+  }
+
+  // ---- requests before any wait: the query features of this wavefront's
+  // two k-steps and the wavefront's page of each step (lane k: step k) ----
+  const int r = c & (kSmRows - 1);
+  const bool row_ok = r < rows;
+  floatx4 x[4];
+  {
+    // k-steps 2w, 2w + 1 of lane group G: features 128 (G & 1) + 64 (G >> 1) + 16w .. + 15
+    const int row = row_ok ? r : 0;
+    const int j = row / a.group, h = kvh * a.group + (row - j * a.group);
+    const floatx4* src = reinterpret_cast<const floatx4*>(
+        a.q + ((int64_t)(it.qa + j) * a.num_heads + h) * kHeadDim + 128 * (G & 1) + 64 * (G >> 1) + 16 * w);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) x[k] = src[k];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  int pgv;
+  {
+    const int32_t* bt_row = a.block_table + (int64_t)it.req * a.bt_stride;
+    const uint32_t tok0 = (uint32_t)(split + nsplit * lane) * kStepTok + kTile * w;
+    const uint32_t pidx = fast_div(tok0, a.bs_div);
+    const bool ok = lane < nst && (int)tok0 < prefix && (int)pidx < a.bt_cols;
+    const int p = bt_row[ok ? pidx : 0];
+    pgv = ok ? p : -1;
+  }
+  auto tile_page = [&](int k) {
+    const int p = __builtin_amdgcn_readlane(pgv, k);
+    return (p >= 0 && p < a.num_pages) ? p : -1;
+  };
+  auto tile_pos = [&](int k) { return (split + nsplit * k) * kStepTok + kTile * w; };
+  auto issue = [&](int k) {
+    load_small_tile(a, S.ring[w][k % kSmRing], tile_page(k), tile_pos(k), prefix, kvh, lane);
+  };
+
+  // ---- Q^T operands (column c: high part of row c, or low part of row c - 8)
+  // of k-steps 2w and 2w + 1 into LDS, and the wavefront's share of the q sums ----
+  {
+    const bool lo = c >= kSmRows;
+#pragma unroll
+    for (int aa = 0; aa < 2; ++aa) {
+      half8 v;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int f = 4 * aa + (u >> 1) + 8 * (u & 1);
+        const float xq = x[f >> 2][f & 3];
+        const _Float16 hi = (_Float16)xq;
+        const _Float16 lw = (_Float16)(xq - (float)hi);
+        v[u] = row_ok ? (lo ? lw : hi) : (_Float16)0.f;
+      }
+      S.qt[2 * w + aa][lane] = v;
+    }
+    float qs = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) qs += (x[k][0] + x[k][1]) + (x[k][2] + x[k][3]);
+    qs = across_groups<false>(qs);
+    if (lane < kSmRows) S.qs[w][lane] = row_ok ? qs : 0.f;
+  }
+  // the first two tiles (the page reads above are complete by now)
+  issue(0);
+  if (nst > 1) issue(1);
+  lds_barrier();
+  const float qsum = (S.qs[0][r] + S.qs[1][r]) + (S.qs[2][r] + S.qs[3][r]);
+
+  floatx4 acc[16];                 // O^T tile n = 4q + 2mh + b
+#pragma unroll
+  for (int n = 0; n < 16; ++n) acc[n] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -__builtin_inff();
+  float l_run = 0.f, z_run = 0.f, ps_run = 0.f;     // this lane's share (its 8 tokens) of row r's sums
+  const uint32_t ones16 = magic_ones();
+  const uint32_t e2 = 2u * (uint32_t)(c & 1);
+  const uint32_t ls0 = 8u - e2, rs0 = e2, ls1 = 4u - e2, rs1 = 4u + e2;
+  SmallTileLds& T = S.tile[w];
+  constexpr int kSlotTok[8] = {0, 2, 1, 3, 4, 6, 5, 7};   // PV k-slot u holds token 8G + kSlotTok[u]
+
+  // The tile's row maximum mb (this lane's row) against the running maximum:
+  // raised lazily (only when it grows by more than 2^kLazy, or at once when
+  // `eager`), rescaling the accumulators and sums; returns the exponent base.
+  auto raise_max = [&](float mb, bool eager) {
+    mb = across_groups<true>(mb);
+    const bool need = mb > m_run + (eager ? 0.f : kLazy);
+    const bool resc = need && m_run != -__builtin_inff();
+    if (__ballot(resc)) {
+      const float alpha = resc ? exp2_raw(m_run - mb) : 1.f;
+#pragma unroll
+      for (int n = 0; n < 16; ++n) acc[n] *= alpha;
+      l_run *= alpha;
+      z_run *= alpha;
+      ps_run *= alpha;
+    }
+    if (need) m_run = mb;
+    return m_run == -__builtin_inff() ? 0.f : m_run;
+  };
+
+  // One tile of INT2 tokens.  Window-owned tokens (bits of wm) are left out
+  // here (score -inf, no weight) and added by the window pass after the loop.
+  auto tile_body = [&](const SmallSlot& L, int k, int nvalid, uint32_t wm) {
+    // Tile k + 2 goes into the slot tile k - 1 left (its LDS reads are complete: lgkmcnt(0)).
+    if (k + 2 < nst) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      asm volatile("" ::: "memory");
+      issue(k + 2);
+    }
+    // ---- token parameters (lane t32 < 32) and the byte-transposed V codes ----
+    bool big;
+    {
+      const bool used = t32 < nvalid && !((wm >> t32) & 1u);
+      const u32x2 meta = L.meta[t32];
+      const float ksc = f16_bits_to_f32(meta[0]);
+      const float kz = f16_bits_to_f32(meta[0] >> 16);
+      const float vsc = f16_bits_to_f32(meta[1]);
+      const float vz = f16_bits_to_f32(meta[1] >> 16);
+      if (lane < kTile) {
+        const float rvs = used ? 1.f / vsc : 0.f;
+        T.prm[0][t32] = used ? 4.f * ksc * a.scale_log2 : 0.f;
+        T.prm[1][t32] = used ? (kz - 4.f * ksc) * a.scale_log2 : 0.f;
+        T.prm[2][t32] = used ? 0.f : -__builtin_inff();
+        T.prm[3][t32] = used ? vsc : 0.f;
+        T.prm[4][t32] = rvs;
+        T.prm[5][t32] = used ? vz * rvs : 0.f;
+      }
+      big = __ballot(used && vsc > kLazyVsMax) != 0;
+      const int tq = lane & 7, bg = lane >> 3;
+      u32x2 vc[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) vc[kk] = *reinterpret_cast<const u32x2*>(&L.vc[4 * tq + kk][8 * bg]);
+      uint32_t o0[4], o1[4];
+      transpose4(vc[0][0], vc[1][0], vc[2][0], vc[3][0], o0);
+      transpose4(vc[0][1], vc[1][1], vc[2][1], vc[3][1], o1);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        T.vt[(8 * bg + kk) * kSmVtRow + tq] = o0[kk];
+        T.vt[(8 * bg + 4 + kk) * kSmVtRow + tq] = o1[kk];
+      }
+    }
+
+    // ---- S^T = K Q^T, both halves ----
+    floatx4 sc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+    const u32x4 kc0 = L.kc[0][lane], kc1 = L.kc[1][lane];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const half8 qa0 = S.qt[2 * jj][lane], qa1 = S.qt[2 * jj + 1][lane];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        half8 ka[2];
+        k_operands(h == 0 ? kc0[jj] : kc1[jj], ones16, ka);
+        sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[0], qa0, sc[h], 0, 0, 0);
+        sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[1], qa1, sc[h], 0, 0, 0);
+      }
+    }
+    wave_sync_lds();
+
+    // ---- scores of tokens 8G + 4h + i for row r, the tile's row maximum ----
+    float sv[8];
+    float mb = -__builtin_inff();
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const floatx4 av = *reinterpret_cast<const floatx4*>(&T.prm[0][8 * G + 4 * h]);
+      const floatx4 bv = *reinterpret_cast<const floatx4*>(&T.prm[1][8 * G + 4 * h]);
+      const floatx4 tmv = *reinterpret_cast<const floatx4*>(&T.prm[2][8 * G + 4 * h]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = ror8_add(sc[h][i]);
+        sv[4 * h + i] = fmaf(av[i], v, bv[i] * qsum) + tmv[i];
+        mb = fmaxf(mb, sv[4 * h + i]);
+      }
+    }
+    const float m_use = raise_max(mb, big);
+
+    // ---- P' = p * vs in the PV token order ----
+    half8 pop;
+    {
+      const floatx4 vs0 = *reinterpret_cast<const floatx4*>(&T.prm[3][8 * G]);
+      const floatx4 vs1 = *reinterpret_cast<const floatx4*>(&T.prm[3][8 * G + 4]);
+      const floatx4 rv0 = *reinterpret_cast<const floatx4*>(&T.prm[4][8 * G]);
+      const floatx4 rv1 = *reinterpret_cast<const floatx4*>(&T.prm[4][8 * G + 4]);
+      const floatx4 zv0 = *reinterpret_cast<const floatx4*>(&T.prm[5][8 * G]);
+      const floatx4 zv1 = *reinterpret_cast<const floatx4*>(&T.prm[5][8 * G + 4]);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int t = kSlotTok[u];
+        const float p = exp2_raw(sv[t] - m_use);
+        const float vs = t < 4 ? vs0[t] : vs1[t - 4];
+        const float rv = t < 4 ? rv0[t] : rv1[t - 4];
+        const float zv = t < 4 ? zv0[t] : zv1[t - 4];
+        const _Float16 hp = (_Float16)(p * vs);
+        pop[u] = hp;
+        const float wh = (float)hp;
+        ps_run += wh;
+        l_run = fmaf(wh, rv, l_run);
+        z_run = fmaf(wh, zv, z_run);
+      }
+    }
+
+    // ---- O^T += V^T P'^T over the 16 feature tiles ----
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int mh = 0; mh < 2; ++mh) {
+        const int brow = 16 * q + 8 * mh + (c >> 1);
+        const u32x2 d = *reinterpret_cast<const u32x2*>(&T.vt[brow * kSmVtRow + 2 * G]);
+        const half8 v0 = as_half8(pair_lo(d[0], ls0, ones16), pair_hi(d[0], rs0, ones16),
+                                  pair_lo(d[1], ls0, ones16), pair_hi(d[1], rs0, ones16));
+        const half8 v1 = as_half8(pair_lo(d[0], ls1, ones16), pair_hi(d[0], rs1, ones16),
+                                  pair_lo(d[1], ls1, ones16), pair_hi(d[1], rs1, ones16));
+        acc[4 * q + 2 * mh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v0, pop, acc[4 * q + 2 * mh], 0, 0, 0);
+        acc[4 * q + 2 * mh + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v1, pop, acc[4 * q + 2 * mh + 1], 0, 0, 0);
+      }
+    }
+  };
+
+  // window-owned tokens of tile k, from its owner tags (bit t: token t)
+  auto window_bits = [&](int k, int own) -> uint32_t {
+    if (!arena) return 0u;
+    const int page = tile_page(k);
+    const int pos = tile_pos(k) + t32;
+    const bool st = page >= 0 && pos < prefix && (pos < win_head || pos >= win_tail) && own == page;
+    return (uint32_t)__ballot(st);
+  };
+
+  uint64_t wtiles = 0;             // tiles k of this wavefront that hold window tokens
+#pragma unroll 1
+  for (int k = 0; k < nst; ++k) {
+    // Wait for tile k's loads, leaving tile k + 1's in flight (tile k + 2 is
+    // requested in the tile body).
+    if (k + 1 < nst)
+      wait_vmcnt<kSmallLoadsPerTile>();
+    else
+      wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    const SmallSlot& L = S.ring[w][k % kSmRing];
+    const int page = tile_page(k);
+    const int nvalid = page >= 0 ? min(kTile, max(prefix - tile_pos(k), 0)) : 0;
+    const uint32_t wm = window_bits(k, (int)L.own[t32][0]);
+    if (wm != 0u) {
+      wtiles |= 1ull << k;
+      S.wbits[w][k] = wm;
+    }
+    tile_body(L, k, nvalid, wm);
+  }
+
+  // ---- the window tokens: K from the fp16 image (high and low parts), V
+  // from the V image, probabilities p / 4 into the same accumulators ----
+#pragma unroll 1
+  while (wtiles != 0ull) {
+    const int k = __builtin_ctzll(wtiles);
+    wtiles &= wtiles - 1;
+    const int page = tile_page(k);
+    const int prow0 = (int)fast_mod((uint32_t)tile_pos(k), a.bs_div);
+    const uint32_t wm = __builtin_amdgcn_readfirstlane(S.wbits[w][k]);
+    const int64_t img = image_index(a, page, prow0, kvh);
+    const u32x4* kimg = reinterpret_cast<const u32x4*>(a.kimg + img * kKImgHalfs);
+    const int il = 8 * (c >> 2) + (c & 3) + 32 * (G & 1);      // image lane of half 0's token
+    // Both parts of both halves at once, zero for tokens outside the window.
+    u32x4 khi[2][8], klo[2][8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const bool wl = (wm >> (8 * (c >> 2) + 4 * h + (c & 3))) & 1u;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        khi[h][s] = wl ? kimg[(8 * (G >> 1) + s) * 64 + il + 4 * h] : u32x4{};
+        klo[h][s] = wl ? kimg[kImgHalfs / 8 + (8 * (G >> 1) + s) * 64 + il + 4 * h] : u32x4{};
+      }
+    }
+    floatx4 sc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const half8 qa = S.qt[s][lane];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, khi[h][s]), qa, sc[h], 0, 0, 0);
+    }
+    // the V image (feature tile n = 4q + 2mh + b: chunk (q, b, G >> 1), lane
+    // 16 mh + c + 32 (G & 1)) requested as soon as the high parts are used,
+    // into their registers (kept below the high-part MFMAs)
+    __builtin_amdgcn_sched_barrier(0);
+    const half8* vimg = reinterpret_cast<const half8*>(a.vimg + img * kImgHalfs);
+    half8 vv[16];
+#pragma unroll
+    for (int n = 0; n < 16; ++n)
+      vv[n] = vimg[(((n >> 2) * 2 + (n & 1)) * 2 + (G >> 1)) * 64 + 16 * ((n >> 1) & 1) + c + 32 * (G & 1)];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const half8 qa = S.qt[s][lane];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, klo[h][s]), qa, sc[h], 0, 0, 0);
+    }
+    float sv[8];
+    float mb = -__builtin_inff();
+    const uint32_t wb = wm >> (8 * G);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = ror8_add(sc[h][i]) * a.scale_log2;
+        sv[4 * h + i] = ((wb >> (4 * h + i)) & 1u) ? v : -__builtin_inff();
+        mb = fmaxf(mb, sv[4 * h + i]);
+      }
+    const float m_use = raise_max(mb, false);
+    half8 pwop;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const _Float16 hw = (_Float16)(0.25f * exp2_raw(sv[kSlotTok[u]] - m_use));
+      pwop[u] = hw;
+      l_run = fmaf(4.f, (float)hw, l_run);
+    }
+#pragma unroll
+    for (int n = 0; n < 16; ++n) acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv[n], pwop, acc[n], 0, 0, 0);
+  }
+
+  // ---- the four wavefronts' rows combined into the split's partial ----
+  l_run = across_groups<false>(l_run);
+  z_run = across_groups<false>(z_run);
+  ps_run = across_groups<false>(ps_run);
+  lds_barrier();                                   // every wavefront is past its last tile
+  SmallCombineLds& C = *reinterpret_cast<SmallCombineLds*>(smem_raw);
+  if (lane < kSmRows) C.m[w][lane] = m_run;
+  lds_barrier();
+  float M = C.m[0][r];
+#pragma unroll
+  for (int ww = 1; ww < kWaves; ++ww) M = fmaxf(M, C.m[ww][r]);
+  const float alpha = m_run == -__builtin_inff() ? 0.f : exp2_raw(m_run - M);
+  // sum_t p (c vs + vz) = 4 * acc - 4 * sum_t P' + sum_t p vz, scaled to the common maximum
+  const float off = alpha * (z_run - 4.f * ps_run);
+  const float a4 = 4.f * alpha;
+  if (c < kSmRows) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int mh = 0; mh < 2; ++mh) {
+        const floatx4 b0 = acc[4 * q + 2 * mh], b1 = acc[4 * q + 2 * mh + 1];
+        float* dst = &C.o[w][c][64 * q + 32 * mh + 8 * G];
+        *reinterpret_cast<floatx4*>(dst) =
+            floatx4{fmaf(a4, b0[0], off), fmaf(a4, b0[1], off), fmaf(a4, b1[0], off), fmaf(a4, b1[1], off)};
+        *reinterpret_cast<floatx4*>(dst + 4) =
+            floatx4{fmaf(a4, b0[2], off), fmaf(a4, b0[3], off), fmaf(a4, b1[2], off), fmaf(a4, b1[3], off)};
+      }
+    }
+    if (G == 0) C.l[w][c] = alpha * l_run;
+  }
+  lds_barrier();
+  // wavefront w: features 64w .. 64w + 63 of every row; lane: row lane / 8, 8 features
+  const int nrow = min(kSmRows, rows);
+  float* part = a.ws + item_index(a, item, split, 0) * kPartialFloats;
+  {
+    const int row = lane >> 3, f = 64 * w + 8 * (lane & 7);
+    if (row < nrow) {
+      floatx4 s0 = *reinterpret_cast<const floatx4*>(&C.o[0][row][f]);
+      floatx4 s1 = *reinterpret_cast<const floatx4*>(&C.o[0][row][f + 4]);
+#pragma unroll
+      for (int ww = 1; ww < kWaves; ++ww) {
+        s0 += *reinterpret_cast<const floatx4*>(&C.o[ww][row][f]);
+        s1 += *reinterpret_cast<const floatx4*>(&C.o[ww][row][f + 4]);
+      }
+      *reinterpret_cast<floatx4*>(part + row * kHeadDim + f) = s0;
+      *reinterpret_cast<floatx4*>(part + row * kHeadDim + f + 4) = s1;
+    }
+    if (w == 0 && lane < nrow) {
+      part[kPartO + lane] = M;
+      part[kPartO + kRows + lane] = (C.l[0][lane] + C.l[1][lane]) + (C.l[2][lane] + C.l[3][lane]);
+    }
+  }
+  if (fresh_here) {
+    __syncthreads();
+    const int ftid = 64 * w + (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    fresh_partial(a, it, item, 0, *reinterpret_cast<FreshLds*>(smem_raw), ftid);
+  }
+}
+
 // One 256-thread block per (output row, quarter of the features) of an item.
 // Every load the block needs goes out in one round: the partials' (m, l)
 // (thread per partial) and the block's 64-feature slice of every partial row
@@ -1482,9 +2023,10 @@ std::atomic<uint64_t> g_split_lds_set[3] = {{0}, {0}, {0}};
 int set_split_lds() {
   const void* k[3] = {reinterpret_cast<const void*>(paged_decode_split_kernel<false, false>),
                       reinterpret_cast<const void*>(paged_decode_split_kernel<true, false>),
-                      reinterpret_cast<const void*>(paged_decode_split_kernel<true, true>)};
+                      reinterpret_cast<const void*>(paged_decode_split_small_kernel)};
+  const size_t bytes[3] = {kLdsBytes, kLdsBytes, kSmallLdsBytes};
   for (int i = 0; i < 3; ++i) {
-    const int rc = set_dynamic_lds(k[i], (int)kLdsBytes, g_split_lds_set[i]);
+    const int rc = set_dynamic_lds(k[i], (int)bytes[i], g_split_lds_set[i]);
     if (rc != kOk) return rc;
   }
   return kOk;
@@ -1501,8 +2043,8 @@ void launch_split(const DecodeArgs& a, unsigned nitems, dim3 grid, hipStream_t s
     if (steps > a.max_splits) multi = true;
     if ((int64_t)a.items[i].nq * a.group > 8) small = false;
   }
-  if (multi && small)
-    hipLaunchKernelGGL((paged_decode_split_kernel<true, true>), grid, dim3(256), kLdsBytes, stream, a);
+  if (small)
+    hipLaunchKernelGGL(paged_decode_split_small_kernel, grid, dim3(256), kSmallLdsBytes, stream, a);
   else if (multi)
     hipLaunchKernelGGL((paged_decode_split_kernel<true, false>), grid, dim3(256), kLdsBytes, stream, a);
   else
