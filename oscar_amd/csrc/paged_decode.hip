@@ -89,10 +89,12 @@ constexpr int kMaxInlineItems = 128;
 
 struct ItemInfo {
   int32_t qa;        // first query row (token) of the request
-  int32_t nq;        // query tokens of the request
   int32_t prefix;    // history length
+  int32_t pbase;     // first partial slot of the item: history splits 0 .. nsplit - 1, then the fresh one
+  int16_t nq;        // query tokens of the request
   int16_t req;       // block-table row (request index within the launch chunk)
   int16_t kvh;       // kv head
+  int16_t nsplit;    // history splits of the item: split s takes steps s, s + nsplit, s + 2 nsplit, ...
 };
 
 struct DecodeArgs {
@@ -119,8 +121,9 @@ struct DecodeArgs {
   float* ws;                    // partials
   const int32_t* win;           // DecodeOnly: (head, cut) per chunk request; null: every position
   int32_t fresh;                // 1: the fresh-token partial exists (MTP read); 0: DecodeOnly
-  int32_t fresh_block;          // 1: a workgroup of its own computes it (x = max_splits); 0: a history split does
-  int32_t max_splits, row_tiles;
+  int32_t fresh_block;          // 1: a workgroup of its own computes it (x = the item's nsplit); 0: a history split does
+  int32_t max_splits, row_tiles;  // the largest nsplit of the launch; row tiles per item
+  int32_t nitems;               // items of the launch chunk
   ItemInfo items[kMaxInlineItems];
 };
 
@@ -161,8 +164,25 @@ static_assert(kLdsBytes <= 80 * 1024, "two workgroups' LDS must fit the CU's 160
 constexpr int kPartO = kRows * kHeadDim;          // row-major O partial
 constexpr size_t kPartialFloats = kPartO + 2 * kRows;
 
-__device__ __forceinline__ int64_t item_index(const DecodeArgs& a, int item, int split, int rt) {
-  return ((int64_t)item * (a.max_splits + 1) + split) * a.row_tiles + rt;
+// The item of split-kernel workgroup b (the split grid is one dimension of
+// exactly the launch's workgroups, item by item: each item's history splits,
+// then its fresh-token workgroup when it has one), and b's index within it.
+// Item i's workgroups start at pbase(i) - i * (fresh - fresh_block), a
+// non-decreasing sequence: the item is the last one whose start is <= b.
+__device__ __forceinline__ int locate_item(const DecodeArgs& a, int b, int& local) {
+  const int skip = a.fresh - a.fresh_block;     // fresh slots without a workgroup of their own
+  int lo = 0, hi = a.nitems - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (a.items[mid].pbase - mid * skip <= b) lo = mid;
+    else hi = mid - 1;
+  }
+  local = b - (a.items[lo].pbase - lo * skip);
+  return lo;
+}
+
+__device__ __forceinline__ int64_t partial_index(const DecodeArgs& a, const ItemInfo& it, int split, int rt) {
+  return ((int64_t)it.pbase + split) * a.row_tiles + rt;
 }
 
 // fp16 pair (1.0, 1.0) held in a VGPR: gfx950's three-operand and-or takes at
@@ -365,7 +385,7 @@ __device__ void fresh_partial(const DecodeArgs& a, const ItemInfo& it, int item,
     }
   }
   if (valid) {
-    float* part = a.ws + item_index(a, item, a.max_splits, rt) * kPartialFloats;
+    float* part = a.ws + partial_index(a, it, it.nsplit, rt) * kPartialFloats;
     float* dst = part + r * kHeadDim + 4 * c;
 #pragma unroll
     for (int k = 0; k < 8; ++k) reinterpret_cast<floatx4*>(dst)[8 * k] = o[k];
@@ -430,17 +450,18 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   // last steps hold the window tokens, whose extra passes make them the
   // longest workgroups, so they start first (measured: C5 decode 37.6 ->
   // 34 us, C2 unchanged).
-  const int bx = blockIdx.x;
-  const int item = blockIdx.y;
+  int bx;
+  const int item = locate_item(a, (int)blockIdx.x, bx);
   const int rt = blockIdx.z;
   const ItemInfo it = a.items[item];
   const int rows = it.nq * a.group;
   if (it.nq <= 0 || rt * kRows >= rows) return;
-  if (a.fresh_block && bx == a.max_splits) {
-    fresh_partial(a, it, item, rt, *reinterpret_cast<FreshLds*>(smem_raw), (int)threadIdx.x);
+  if (bx >= it.nsplit) {                  // the fresh-token workgroup, or none for this item
+    if (a.fresh_block && bx == it.nsplit)
+      fresh_partial(a, it, item, rt, *reinterpret_cast<FreshLds*>(smem_raw), (int)threadIdx.x);
     return;
   }
-  const int split = bx == 0 ? 0 : a.max_splits - bx;
+  const int split = bx == 0 ? 0 : it.nsplit - bx;
   const int prefix = it.prefix;
   const int steps = (prefix + kStepTok - 1) / kStepTok;
   // Without a workgroup of its own (when one more per item would not find a
@@ -450,8 +471,8 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   // split when the history has fewer steps than there are splits; else the
   // last split when the steps do not divide evenly (it has one step fewer
   // than the splits that hold the last steps); else the middle one.
-  const int rem = a.max_splits > 0 ? steps % a.max_splits : 0;
-  const int fresh_split = steps < a.max_splits ? steps : (rem != 0 ? a.max_splits - 1 : a.max_splits / 2);
+  const int rem = steps % it.nsplit;
+  const int fresh_split = steps < it.nsplit ? steps : (rem != 0 ? it.nsplit - 1 : it.nsplit / 2);
   const bool fresh_here = a.fresh && !a.fresh_block && split == fresh_split;
   if (split >= steps) {
     if (fresh_here) fresh_partial(a, it, item, rt, *reinterpret_cast<FreshLds*>(smem_raw), (int)threadIdx.x);
@@ -465,7 +486,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   const int g = lane >> 5;
   const int col = lane & 31;
   const int kvh = it.kvh;
-  const int nsplit = a.max_splits;
+  const int nsplit = it.nsplit;
   const int nst = (steps - 1 - split) / nsplit + 1;     // steps split + nsplit k, k < nst (<= 64)
   const bool arena = a.stage_rows > 0;
   // Positions whose staged value may replace the INT2 one: p < win_head or
@@ -995,7 +1016,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   // Registers 4jq + 2h, 4jq + 2h + 1 of blocks 0 and 1 are local features
   // 16jq + 8g + 4h + 0 .. 3 of row col: stored straight from the registers.
   const int nrow = min(kRows, rows - rt * kRows);
-  float* part = a.ws + item_index(a, item, split, rt) * kPartialFloats;
+  float* part = a.ws + partial_index(a, it, split, rt) * kPartialFloats;
   if (col < nrow) {
     float* dst = part + col * kHeadDim + 64 * w + 8 * g;
 #pragma unroll
@@ -1154,21 +1175,22 @@ __device__ __forceinline__ float ror8_add(float x) {
 
 __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
-  const int bx = blockIdx.x;
-  const int item = blockIdx.y;
+  int bx;
+  const int item = locate_item(a, (int)blockIdx.x, bx);
   const ItemInfo it = a.items[item];
   const int rows = it.nq * a.group;
   if (it.nq <= 0 || blockIdx.z != 0) return;
-  if (a.fresh_block && bx == a.max_splits) {
-    fresh_partial(a, it, item, 0, *reinterpret_cast<FreshLds*>(smem_raw), (int)threadIdx.x);
+  if (bx >= it.nsplit) {                  // the fresh-token workgroup, or none for this item
+    if (a.fresh_block && bx == it.nsplit)
+      fresh_partial(a, it, item, 0, *reinterpret_cast<FreshLds*>(smem_raw), (int)threadIdx.x);
     return;
   }
   // history splits dispatched as 0, S - 1, S - 2, ..., 1 (the window steps first)
-  const int split = bx == 0 ? 0 : a.max_splits - bx;
+  const int split = bx == 0 ? 0 : it.nsplit - bx;
   const int prefix = it.prefix;
   const int steps = (prefix + kStepTok - 1) / kStepTok;
-  const int rem = a.max_splits > 0 ? steps % a.max_splits : 0;
-  const int fresh_split = steps < a.max_splits ? steps : (rem != 0 ? a.max_splits - 1 : a.max_splits / 2);
+  const int rem = steps % it.nsplit;
+  const int fresh_split = steps < it.nsplit ? steps : (rem != 0 ? it.nsplit - 1 : it.nsplit / 2);
   const bool fresh_here = a.fresh && !a.fresh_block && split == fresh_split;
   if (split >= steps) {
     if (fresh_here) fresh_partial(a, it, item, 0, *reinterpret_cast<FreshLds*>(smem_raw), (int)threadIdx.x);
@@ -1180,7 +1202,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(Decode
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15, G = lane >> 4, t32 = lane & 31;
   const int kvh = it.kvh;
-  const int nsplit = a.max_splits;
+  const int nsplit = it.nsplit;
   const int nst = (steps - 1 - split) / nsplit + 1;
   const bool arena = a.stage_rows > 0;
   int win_head = 0, win_tail = 0;
@@ -1533,7 +1555,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(Decode
   lds_barrier();
   // wavefront w: features 64w .. 64w + 63 of every row; lane: row lane / 8, 8 features
   const int nrow = min(kSmRows, rows);
-  float* part = a.ws + item_index(a, item, split, 0) * kPartialFloats;
+  float* part = a.ws + partial_index(a, it, split, 0) * kPartialFloats;
   {
     const int row = lane >> 3, f = 64 * w + 8 * (lane & 7);
     if (row < nrow) {
@@ -1548,6 +1570,533 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(Decode
       *reinterpret_cast<floatx4*>(part + row * kHeadDim + f + 4) = s1;
     }
     if (w == 0 && lane < nrow) {
+      part[kPartO + lane] = M;
+      part[kPartO + kRows + lane] = (C.l[0][lane] + C.l[1][lane]) + (C.l[2][lane] + C.l[3][lane]);
+    }
+  }
+  if (fresh_here) {
+    __syncthreads();
+    const int ftid = 64 * w + (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    fresh_partial(a, it, item, 0, *reinterpret_cast<FreshLds*>(smem_raw), ftid);
+  }
+}
+
+// ---------------------------------------------------------------- wide split kernel
+// Multi-step launches whose items have 9 to 24 rows (MTP steps of a few
+// tokens over a GQA group, e.g. 4 tokens x 6 heads): the small-row kernel's
+// structure (each wavefront walks its own 32-token tiles with its own
+// running maxima and sums, a per-wavefront LDS ring of tiles filled by
+// buffer loads to LDS, window tokens in a pass of their own after the loop)
+// on v_mfma_f32_32x32x16_f16 tiles of 32 tokens x 32 rows.  Lane l = (j, g),
+// j = l % 32, g = l / 32:
+//  * S^T = K Q^T: A = K: lane (t, g) holds token pi(t) (pi swaps bits 2 and 3
+//    of t) with the features of window-image block m, half g; B = Q^T (high
+//    part, then low part, from LDS).  Result register r of lane (j, g) is the
+//    score of token 16 (r >> 3) + 8g + 4 ((r >> 2) & 1) + (r & 3) for row j,
+//    so that lane group g holds tokens 8g .. 8g + 7 of each 16-token k-step
+//    of the PV pass, exactly the token grouping of the window V image.
+//  * O^T += V^T P'^T: A = V^T: lane (m, g) holds feature 64q + 4 (m >> 1) + 2b
+//    + (m & 1) of tokens 16s + 8g + {0, 2, 1, 3, 4, 6, 5, 7} (k-step s), B =
+//    P'^T in the same order straight from the score registers.  Output
+//    registers 4jq + 2h + e of blocks (q, b) are features 64q + 16jq + 8g + 4h
+//    + 2b + e of row j: the whole 256 features x 32 rows in 128 registers.
+constexpr int kWdRows = 24;
+constexpr int kWdRing = 2;       // tiles resident per wavefront: the one computed and one in flight
+
+struct WideLds {
+  _Float16 q[16 * 2 * kWdRows * 8];        // Q^T operand [m][g][row][8], fp16 high part
+  _Float16 qlo[16 * 2 * kWdRows * 8];      // low part fp16(q - high)
+  float qsum[kWdRows];
+  SmallTileLds tile[kWaves];
+  uint32_t wbits[kWaves][kMaxTilesPerSplit / kWaves];
+  SmallSlot ring[kWaves][kWdRing];
+};
+
+struct WideCombineLds {
+  float o[2][kWdRows][kHeadDim];           // two wavefronts' scaled rows
+  float m[kWaves][kRows];
+  float l[kWaves][kRows];
+};
+
+constexpr size_t kWideLdsBytes = sizeof(WideLds) > sizeof(WideCombineLds)
+                                     ? (sizeof(WideLds) > sizeof(FreshLds) ? sizeof(WideLds) : sizeof(FreshLds))
+                                     : (sizeof(WideCombineLds) > sizeof(FreshLds) ? sizeof(WideCombineLds)
+                                                                                  : sizeof(FreshLds));
+static_assert(kWideLdsBytes <= 80 * 1024, "two workgroups' LDS must fit the CU's 160 KiB");
+
+__device__ __forceinline__ int swap23(int t) { return (t & ~12) | ((t & 4) << 1) | ((t & 8) >> 1); }
+
+// The wide kernel's tile loads: as load_small_tile, with lane (t, g) copying
+// the 32 K code bytes 32g .. 32g + 31 of token pi(t) in two 16-byte loads.
+__device__ __forceinline__ void load_wide_tile(const DecodeArgs& a, SmallSlot& slot, int page, int p0, int prefix,
+                                               int kvh, int lane) {
+  const int t = lane & 31, g = lane >> 5;
+  const bool tile_ok = p0 < prefix && page >= 0;
+  const int pgc = tile_ok ? page : 0;
+  const int prow0 = (int)fast_mod((uint32_t)p0, a.bs_div);
+  const int nrow = tile_ok ? min(kTile, prefix - p0) : 0;
+  auto row_of = [&](int tk) { return tk < nrow ? prow0 + tk : 0; };
+  const uint32_t krec = (uint32_t)((int64_t)(a.block_size - 1) * a.k_tok + kKCodeOff + kCodeBytes);
+  const uint32_t vrec = (uint32_t)((int64_t)(a.block_size - 1) * a.v_tok + kCodeBytes);
+  const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.k_cache + (int64_t)pgc * a.k_page + (int64_t)kvh * a.k_head), (short)0, krec, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.v_cache + (int64_t)pgc * a.v_page + (int64_t)kvh * a.v_head), (short)0, vrec, 0x00020000);
+  const int krow = row_of(swap23(t)) * (int)a.k_tok + kKCodeOff + 32 * g;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void*)&slot.kc[h][0], 16, krow + 16 * h, 0, 0, 0);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int tk = 16 * i + (lane >> 2);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_void*)&slot.vc[16 * i][0], 16,
+                                             row_of(tk) * (int)a.v_tok + 16 * (lane & 3), 0, 0, 0);
+  }
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void*)&slot.meta[0], 4,
+                                           row_of(lane >> 1) * (int)a.k_tok + 4 * (lane & 1), 0, 0, 0);
+  const bool arena = a.stage_rows > 0;
+  const int64_t seat0 = arena ? (int64_t)fast_mod((uint32_t)pgc, a.rows_div) * a.block_size + prow0 : 0;
+  const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc(
+      arena ? (void*)(a.owner + seat0) : (void*)a.k_cache, (short)0, arena ? (uint32_t)(kTile * 8) : 0u,
+      0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(orr, (lds_void*)&slot.own[0], 4, 4 * lane, 0, 0, 0);
+}
+
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return fmaxf(__int_as_float(s32[0]), __int_as_float(s32[1]));
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return __int_as_float(s32[0]) + __int_as_float(s32[1]);
+}
+
+__global__ __launch_bounds__(256, 2) void paged_decode_split_wide_kernel(DecodeArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
+  int bx;
+  const int item = locate_item(a, (int)blockIdx.x, bx);
+  const ItemInfo it = a.items[item];
+  const int rows = it.nq * a.group;
+  if (it.nq <= 0 || blockIdx.z != 0) return;
+  if (bx >= it.nsplit) {                  // the fresh-token workgroup, or none for this item
+    if (a.fresh_block && bx == it.nsplit)
+      fresh_partial(a, it, item, 0, *reinterpret_cast<FreshLds*>(smem_raw), (int)threadIdx.x);
+    return;
+  }
+  const int split = bx == 0 ? 0 : it.nsplit - bx;
+  const int prefix = it.prefix;
+  const int steps = (prefix + kStepTok - 1) / kStepTok;
+  const int rem = steps % it.nsplit;
+  const int fresh_split = steps < it.nsplit ? steps : (rem != 0 ? it.nsplit - 1 : it.nsplit / 2);
+  const bool fresh_here = a.fresh && !a.fresh_block && split == fresh_split;
+  if (split >= steps) {
+    if (fresh_here) fresh_partial(a, it, item, 0, *reinterpret_cast<FreshLds*>(smem_raw), (int)threadIdx.x);
+    return;
+  }
+  WideLds& S = *reinterpret_cast<WideLds*>(smem_raw);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 31, g = lane >> 5;
+  const int kvh = it.kvh;
+  const int nsplit = it.nsplit;
+  const int nst = (steps - 1 - split) / nsplit + 1;
+  const bool arena = a.stage_rows > 0;
+  int win_head = 0, win_tail = 0;
+  if (a.win) {
+    typedef __attribute__((address_space(4))) const int32_t const_i32;
+    const const_i32* wb = (const const_i32*)a.win;
+    win_head = wb[2 * it.req];
+    win_tail = wb[2 * it.req + 1];
+  }
+
+  // ---- requests before any wait: the query features (thread: row r8,
+  // features 32 c8 .. + 31) and the wavefront's page of each step ----
+  const int r8 = tid >> 3, c8 = tid & 7;
+  floatx4 x[8];
+  {
+    const int row = r8 < rows ? r8 : rows - 1;
+    const int jq = row / a.group, h = kvh * a.group + (row - jq * a.group);
+    const floatx4* src = reinterpret_cast<const floatx4*>(a.q + ((int64_t)(it.qa + jq) * a.num_heads + h) *
+                                                          kHeadDim + 32 * c8);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) x[k] = src[k];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  int pgv;
+  {
+    const int32_t* bt_row = a.block_table + (int64_t)it.req * a.bt_stride;
+    const uint32_t tok0 = (uint32_t)(split + nsplit * lane) * kStepTok + kTile * w;
+    const uint32_t pidx = fast_div(tok0, a.bs_div);
+    const bool ok = lane < nst && (int)tok0 < prefix && (int)pidx < a.bt_cols;
+    const int p = bt_row[ok ? pidx : 0];
+    pgv = ok ? p : -1;
+  }
+  auto tile_page = [&](int k) {
+    const int p = __builtin_amdgcn_readlane(pgv, k);
+    return (p >= 0 && p < a.num_pages) ? p : -1;
+  };
+  auto tile_pos = [&](int k) { return (split + nsplit * k) * kStepTok + kTile * w; };
+  auto issue = [&](int k) {
+    load_wide_tile(a, S.ring[w][k % kWdRing], tile_page(k), tile_pos(k), prefix, kvh, lane);
+  };
+
+  // ---- Q^T operand (permuted K dimension, fp16 high + low parts) and row sums ----
+  // Thread (r8, c8): features 32 c8 .. + 31 of row r8 are the four operand
+  // vectors (m = 2 (2 (c8 & 3) + jl) + aa, half c8 >> 2); slot 2i + b of
+  // vector (jl, aa) is local feature 16 jl + 4 aa + i + 8b.
+  {
+    float qs = 0.f;
+    const int gg = c8 >> 2;
+#pragma unroll
+    for (int jl = 0; jl < 2; ++jl) {
+#pragma unroll
+      for (int aa = 0; aa < 2; ++aa) {
+        half8 v, vl;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int k = 16 * jl + 4 * aa + (u >> 1) + 8 * (u & 1);
+          const float xq = x[k >> 2][k & 3];
+          v[u] = (_Float16)xq;
+          vl[u] = (_Float16)(xq - (float)v[u]);
+          qs += xq;
+        }
+        const int m = 2 * (2 * (c8 & 3) + jl) + aa;
+        if (r8 < kWdRows) {
+          const bool ok = r8 < rows;
+          *reinterpret_cast<half8*>(&S.q[((m * 2 + gg) * kWdRows + r8) * 8]) = ok ? v : half8{};
+          *reinterpret_cast<half8*>(&S.qlo[((m * 2 + gg) * kWdRows + r8) * 8]) = ok ? vl : half8{};
+        }
+      }
+    }
+    qs += shfl_xor_f32(qs, 1);
+    qs += shfl_xor_f32(qs, 2);
+    qs += shfl_xor_f32(qs, 4);
+    if (c8 == 0 && r8 < kWdRows) S.qsum[r8] = r8 < rows ? qs : 0.f;
+  }
+  issue(0);
+  lds_barrier();
+  const float qsum = j < kWdRows ? S.qsum[j] : 0.f;
+  const bool qrow = j < kWdRows;
+  auto qop = [&](int m, bool lo) -> half8 {
+    const _Float16* base = lo ? S.qlo : S.q;
+    return qrow ? *reinterpret_cast<const half8*>(&base[((m * 2 + g) * kWdRows + j) * 8]) : half8{};
+  };
+
+  floatx16 acc[4][2];              // O^T blocks (q, b)
+#pragma unroll
+  for (int q = 0; q < 4; ++q) acc[q][0] = acc[q][1] = floatx16{};
+  float m_run = -__builtin_inff();
+  float l_run = 0.f, z_run = 0.f, ps_run = 0.f;     // this lane's share (its 16 tokens) of row j's sums
+  const uint32_t ones16 = magic_ones();
+  const uint32_t e2 = 2u * (uint32_t)(j & 1);
+  const uint32_t ls0 = 8u - e2, rs0 = e2, ls1 = 4u - e2, rs1 = 4u + e2;
+  SmallTileLds& T = S.tile[w];
+  constexpr int kSlotTok[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+  // score register of token 16s + 8g + v (v < 8) in lane group g
+  auto reg_of = [](int s, int v) { return 8 * s + v; };
+
+  auto raise_max = [&](float mb, bool eager) {
+    mb = xor32_max(mb);
+    const bool need = mb > m_run + (eager ? 0.f : kLazy);
+    const bool resc = need && m_run != -__builtin_inff();
+    if (__ballot(resc)) {
+      const float alpha = resc ? exp2_raw(m_run - mb) : 1.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc[q][0] *= alpha;
+        acc[q][1] *= alpha;
+      }
+      l_run *= alpha;
+      z_run *= alpha;
+      ps_run *= alpha;
+    }
+    if (need) m_run = mb;
+    return m_run == -__builtin_inff() ? 0.f : m_run;
+  };
+
+  auto tile_body = [&](const SmallSlot& L, int k, int nvalid, uint32_t wm) {
+    // Tile k + 1 goes into the slot tile k - 1 left (its LDS reads are complete: lgkmcnt(0)).
+    if (k + 1 < nst) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      asm volatile("" ::: "memory");
+      issue(k + 1);
+    }
+    // ---- token parameters (lane t < 32) and the byte-transposed V codes ----
+    bool big;
+    {
+      const int t = lane & 31;
+      const bool used = t < nvalid && !((wm >> t) & 1u);
+      const u32x2 meta = L.meta[t];
+      const float ksc = f16_bits_to_f32(meta[0]);
+      const float kz = f16_bits_to_f32(meta[0] >> 16);
+      const float vsc = f16_bits_to_f32(meta[1]);
+      const float vz = f16_bits_to_f32(meta[1] >> 16);
+      if (lane < kTile) {
+        const float rvs = used ? 1.f / vsc : 0.f;
+        T.prm[0][t] = used ? 4.f * ksc * a.scale_log2 : 0.f;
+        T.prm[1][t] = used ? (kz - 4.f * ksc) * a.scale_log2 : 0.f;
+        T.prm[2][t] = used ? 0.f : -__builtin_inff();
+        T.prm[3][t] = used ? vsc : 0.f;
+        T.prm[4][t] = rvs;
+        T.prm[5][t] = used ? vz * rvs : 0.f;
+      }
+      big = __ballot(used && vsc > kLazyVsMax) != 0;
+      const int tq = lane & 7, bg = lane >> 3;
+      u32x2 vc[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) vc[kk] = *reinterpret_cast<const u32x2*>(&L.vc[4 * tq + kk][8 * bg]);
+      uint32_t o0[4], o1[4];
+      transpose4(vc[0][0], vc[1][0], vc[2][0], vc[3][0], o0);
+      transpose4(vc[0][1], vc[1][1], vc[2][1], vc[3][1], o1);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        T.vt[(8 * bg + kk) * kSmVtRow + tq] = o0[kk];
+        T.vt[(8 * bg + 4 + kk) * kSmVtRow + tq] = o1[kk];
+      }
+    }
+
+    // ---- S^T = K Q^T (both q parts) ----
+    floatx16 sc = floatx16{};
+    const u32x4 kc0 = L.kc[0][lane], kc1 = L.kc[1][lane];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      half8 ka[2];
+      k_operands(jj < 4 ? kc0[jj] : kc1[jj - 4], ones16, ka);
+#pragma unroll
+      for (int aa = 0; aa < 2; ++aa) {
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[aa], qop(2 * jj + aa, false), sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[aa], qop(2 * jj + aa, true), sc, 0, 0, 0);
+      }
+    }
+    wave_sync_lds();
+
+    // ---- scores of row j, tokens 16s + 8g + 4 hh + i (register 8s + 4hh + i) ----
+    float mb = -__builtin_inff();
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int t0 = 16 * s + 8 * g + 4 * hh;
+        const floatx4 av = *reinterpret_cast<const floatx4*>(&T.prm[0][t0]);
+        const floatx4 bv = *reinterpret_cast<const floatx4*>(&T.prm[1][t0]);
+        const floatx4 tmv = *reinterpret_cast<const floatx4*>(&T.prm[2][t0]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int rr = 8 * s + 4 * hh + i;
+          sc[rr] = fmaf(av[i], sc[rr], bv[i] * qsum) + tmv[i];
+          mb = fmaxf(mb, sc[rr]);
+        }
+      }
+    }
+    const float m_use = raise_max(mb, big);
+
+    // ---- P' = p * vs per k-step s, in the PV token order, and O^T += V^T P'^T ----
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      half8 pop;
+      {
+        const int t0 = 16 * s + 8 * g;
+        const floatx4 vs0 = *reinterpret_cast<const floatx4*>(&T.prm[3][t0]);
+        const floatx4 vs1 = *reinterpret_cast<const floatx4*>(&T.prm[3][t0 + 4]);
+        const floatx4 rv0 = *reinterpret_cast<const floatx4*>(&T.prm[4][t0]);
+        const floatx4 rv1 = *reinterpret_cast<const floatx4*>(&T.prm[4][t0 + 4]);
+        const floatx4 zv0 = *reinterpret_cast<const floatx4*>(&T.prm[5][t0]);
+        const floatx4 zv1 = *reinterpret_cast<const floatx4*>(&T.prm[5][t0 + 4]);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int v = kSlotTok[u];
+          const float p = exp2_raw(sc[reg_of(s, v)] - m_use);
+          const float vs = v < 4 ? vs0[v] : vs1[v - 4];
+          const float rv = v < 4 ? rv0[v] : rv1[v - 4];
+          const float zv = v < 4 ? zv0[v] : zv1[v - 4];
+          const _Float16 hp = (_Float16)(p * vs);
+          pop[u] = hp;
+          const float wh = (float)hp;
+          ps_run += wh;
+          l_run = fmaf(wh, rv, l_run);
+          z_run = fmaf(wh, zv, z_run);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x2 d = *reinterpret_cast<const u32x2*>(&T.vt[(16 * q + (j >> 1)) * kSmVtRow + 4 * s + 2 * g]);
+        const half8 v0 = as_half8(pair_lo(d[0], ls0, ones16), pair_hi(d[0], rs0, ones16),
+                                  pair_lo(d[1], ls0, ones16), pair_hi(d[1], rs0, ones16));
+        const half8 v1 = as_half8(pair_lo(d[0], ls1, ones16), pair_hi(d[0], rs1, ones16),
+                                  pair_lo(d[1], ls1, ones16), pair_hi(d[1], rs1, ones16));
+        acc[q][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v0, pop, acc[q][0], 0, 0, 0);
+        acc[q][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v1, pop, acc[q][1], 0, 0, 0);
+      }
+    }
+  };
+
+  auto window_bits = [&](int k, int own) -> uint32_t {
+    if (!arena) return 0u;
+    const int page = tile_page(k);
+    const int pos = tile_pos(k) + (lane & 31);
+    const bool st = page >= 0 && pos < prefix && (pos < win_head || pos >= win_tail) && own == page;
+    return (uint32_t)__ballot(st);
+  };
+
+  uint64_t wtiles = 0;
+#pragma unroll 1
+  for (int k = 0; k < nst; ++k) {
+    // wait for tile k's loads (tile k + 1 is requested in the tile body)
+    wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    const SmallSlot& L = S.ring[w][k % kWdRing];
+    const int page = tile_page(k);
+    const int nvalid = page >= 0 ? min(kTile, max(prefix - tile_pos(k), 0)) : 0;
+    const uint32_t wm = window_bits(k, (int)L.own[lane & 31][0]);
+    if (wm != 0u) {
+      wtiles |= 1ull << k;
+      S.wbits[w][k] = wm;
+    }
+    tile_body(L, k, nvalid, wm);
+  }
+
+  // ---- the window tokens: K from the fp16 image (high and low parts, half
+  // the k-steps at a time), V from the V image, p / 4 into the same accumulators ----
+#pragma unroll 1
+  while (wtiles != 0ull) {
+    const int k = __builtin_ctzll(wtiles);
+    wtiles &= wtiles - 1;
+    const int page = tile_page(k);
+    const int prow0 = (int)fast_mod((uint32_t)tile_pos(k), a.bs_div);
+    const uint32_t wm = __builtin_amdgcn_readfirstlane(S.wbits[w][k]);
+    const int64_t img = image_index(a, page, prow0, kvh);
+    const u32x4* kimg = reinterpret_cast<const u32x4*>(a.kimg + img * kKImgHalfs);
+    const int tl = swap23(j);                                   // this lane's token as an A row
+    const bool wl = (wm >> tl) & 1u;
+    floatx16 sc = floatx16{};
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      u32x4 khi[8], klo[8];
+#pragma unroll
+      for (int mm = 0; mm < 8; ++mm) {
+        const int m = 8 * half + mm;
+        khi[mm] = wl ? kimg[m * 64 + tl + 32 * g] : u32x4{};
+        klo[mm] = wl ? kimg[kImgHalfs / 8 + m * 64 + tl + 32 * g] : u32x4{};
+      }
+#pragma unroll
+      for (int mm = 0; mm < 8; ++mm) {
+        const int m = 8 * half + mm;
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, khi[mm]), qop(m, false), sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, khi[mm]), qop(m, true), sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, klo[mm]), qop(m, false), sc, 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const half8* vimg = reinterpret_cast<const half8*>(a.vimg + img * kImgHalfs);
+    half8 vv[4][2][2];             // block (q, b), k-step s
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) vv[q][b][s] = vimg[((q * 2 + b) * 2 + s) * 64 + lane];
+    float mb = -__builtin_inff();
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) {
+      const int tok = 16 * (rr >> 3) + 8 * g + (rr & 7);
+      sc[rr] = ((wm >> tok) & 1u) ? sc[rr] * a.scale_log2 : -__builtin_inff();
+      mb = fmaxf(mb, sc[rr]);
+    }
+    const float m_use = raise_max(mb, false);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      half8 pwop;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const _Float16 hw = (_Float16)(0.25f * exp2_raw(sc[reg_of(s, kSlotTok[u])] - m_use));
+        pwop[u] = hw;
+        l_run = fmaf(4.f, (float)hw, l_run);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          acc[q][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vv[q][b][s], pwop, acc[q][b], 0, 0, 0);
+    }
+  }
+
+  // ---- the four wavefronts' rows combined into the split's partial:
+  // (w0 + w2) + (w1 + w3), each scaled to the common maximum ----
+  l_run = xor32_sum(l_run);
+  z_run = xor32_sum(z_run);
+  ps_run = xor32_sum(ps_run);
+  lds_barrier();                                   // every wavefront is past its last tile
+  WideCombineLds& C = *reinterpret_cast<WideCombineLds*>(smem_raw);
+  if (lane < kRows) C.m[w][lane] = m_run;
+  lds_barrier();
+  float M = C.m[0][j];
+#pragma unroll
+  for (int ww = 1; ww < kWaves; ++ww) M = fmaxf(M, C.m[ww][j]);
+  const float alpha = m_run == -__builtin_inff() ? 0.f : exp2_raw(m_run - M);
+  // sum_t p (c vs + vz) = 4 * acc - 4 * sum_t P' + sum_t p vz, scaled to the common maximum
+  const float off = alpha * (z_run - 4.f * ps_run);
+  const float a4 = 4.f * alpha;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[q][b][i] = fmaf(a4, acc[q][b][i], off);
+  if (g == 0) C.l[w][j] = alpha * l_run;
+  // registers 4jq + 2h + e of blocks (q, b): features 64q + 16jq + 8g + 4h + 2b + e of row j
+  auto put = [&](int buf) {
+    if (j < kWdRows) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            *reinterpret_cast<floatx4*>(&C.o[buf][j][64 * q + 16 * jq + 8 * g + 4 * h]) =
+                floatx4{acc[q][0][4 * jq + 2 * h], acc[q][0][4 * jq + 2 * h + 1], acc[q][1][4 * jq + 2 * h],
+                        acc[q][1][4 * jq + 2 * h + 1]};
+    }
+  };
+  auto add = [&](int buf) {
+    if (j < kWdRows) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const floatx4 o = *reinterpret_cast<const floatx4*>(&C.o[buf][j][64 * q + 16 * jq + 8 * g + 4 * h]);
+            acc[q][0][4 * jq + 2 * h] += o[0];
+            acc[q][0][4 * jq + 2 * h + 1] += o[1];
+            acc[q][1][4 * jq + 2 * h] += o[2];
+            acc[q][1][4 * jq + 2 * h + 1] += o[3];
+          }
+    }
+  };
+  lds_barrier();                                   // the maxima are read
+  if (w >= 2) put(w - 2);
+  lds_barrier();
+  if (w < 2) add(w);
+  lds_barrier();
+  if (w == 1) put(0);
+  lds_barrier();
+  const int nrow = min(kWdRows, rows);
+  float* part = a.ws + partial_index(a, it, split, 0) * kPartialFloats;
+  if (w == 0) {
+    add(0);
+    if (j < nrow) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            *reinterpret_cast<floatx4*>(part + j * kHeadDim + 64 * q + 16 * jq + 8 * g + 4 * h) =
+                floatx4{acc[q][0][4 * jq + 2 * h], acc[q][0][4 * jq + 2 * h + 1], acc[q][1][4 * jq + 2 * h],
+                        acc[q][1][4 * jq + 2 * h + 1]};
+    }
+    if (lane < nrow) {
       part[kPartO + lane] = M;
       part[kPartO + kRows + lane] = (C.l[0][lane] + C.l[1][lane]) + (C.l[2][lane] + C.l[3][lane]);
     }
@@ -1585,9 +2134,9 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
   const int lane = tid & 63, w = tid >> 6;
   const int sg = tid >> 4, fl = tid & 15;
   const int steps = (it.prefix + kStepTok - 1) / kStepTok;
-  const int hs = min(a.max_splits, steps);        // history partials 0 .. hs - 1
-  const int P = hs + a.fresh;                     // partial hs is the fresh one (split max_splits)
-  const float* base = a.ws + item_index(a, item, 0, rt) * kPartialFloats;
+  const int hs = min((int)it.nsplit, steps);      // history partials 0 .. hs - 1
+  const int P = hs + a.fresh;                     // partial hs is the fresh one (slot nsplit)
+  const float* base = a.ws + partial_index(a, it, 0, rt) * kPartialFloats;
   const int64_t pstride = (int64_t)a.row_tiles * kPartialFloats;
   const int f0 = 64 * qd + 4 * fl;
 
@@ -1599,7 +2148,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
     mreg[k] = -__builtin_inff();
     lreg[k] = 0.f;
     if (p < P) {
-      const float* pp = base + (p < hs ? p : a.max_splits) * pstride;
+      const float* pp = base + (p < hs ? p : it.nsplit) * pstride;
       mreg[k] = pp[kPartO + r];
       lreg[k] = pp[kPartO + kRows + r];
     }
@@ -1608,7 +2157,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
 #pragma unroll
   for (int k = 0; k < kMergeBatch; ++k) {
     const int p = sg + kMergeGroups * k;
-    x[k] = p < P ? *reinterpret_cast<const floatx4*>(base + (p < hs ? p : a.max_splits) * pstride +
+    x[k] = p < P ? *reinterpret_cast<const floatx4*>(base + (p < hs ? p : it.nsplit) * pstride +
                                                      r * kHeadDim + f0)
                  : floatx4{};
   }
@@ -1647,7 +2196,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
 #pragma unroll
     for (int k = 0; k < kMergeBatch; ++k) {
       const int p = s0 + kMergeGroups * k;
-      x[k] = p < P ? *reinterpret_cast<const floatx4*>(base + (p < hs ? p : a.max_splits) * pstride +
+      x[k] = p < P ? *reinterpret_cast<const floatx4*>(base + (p < hs ? p : it.nsplit) * pstride +
                                                        r * kHeadDim + f0)
                    : floatx4{};
     }
@@ -1695,9 +2244,9 @@ __global__ __launch_bounds__(256) void paged_decode_merge_small_kernel(DecodeArg
   const int row = rt * kRows + r;
   if (it.nq <= 0 || r >= kRows || row >= rows) return;
   const int steps = (it.prefix + kStepTok - 1) / kStepTok;
-  const int hs = min(a.max_splits, steps);
+  const int hs = min((int)it.nsplit, steps);
   const int P = hs + a.fresh;
-  const float* base = a.ws + item_index(a, item, 0, rt) * kPartialFloats;
+  const float* base = a.ws + partial_index(a, it, 0, rt) * kPartialFloats;
   const int64_t pstride = (int64_t)a.row_tiles * kPartialFloats;
   const int f0 = 64 * qd + 4 * (tid & 15);
   float m[kSmallP], l[kSmallP];
@@ -1708,7 +2257,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge_small_kernel(DecodeArg
     l[p] = 0.f;
     x[p] = floatx4{};
     if (p < P) {
-      const float* pp = base + (p < hs ? p : a.max_splits) * pstride;
+      const float* pp = base + (p < hs ? p : it.nsplit) * pstride;
       m[p] = pp[kPartO + r];
       l[p] = pp[kPartO + kRows + r];
       x[p] = *reinterpret_cast<const floatx4*>(pp + r * kHeadDim + f0);
@@ -1767,11 +2316,11 @@ __global__ __launch_bounds__(kRotThreads) void paged_decode_merge_rotate_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int steps = (it.prefix + kStepTok - 1) / kStepTok;
-  const int hs = min(a.max_splits, steps);
+  const int hs = min((int)it.nsplit, steps);
   const int P = hs + a.fresh;
-  const float* base = a.ws + item_index(a, item, 0, rt) * kPartialFloats;
+  const float* base = a.ws + partial_index(a, it, 0, rt) * kPartialFloats;
   const int64_t pstride = (int64_t)a.row_tiles * kPartialFloats;
-  auto partial = [&](int p) { return base + (p < hs ? p : a.max_splits) * pstride; };
+  auto partial = [&](int p) { return base + (p < hs ? p : it.nsplit) * pstride; };
 
   // ---- every load of the first round ----
   float rv[kHeadDim / kRotWaves];
@@ -1933,27 +2482,26 @@ int32_t requests_per_launch(int32_t num_kv_heads);
 
 // Split workgroups resident at once: two per CU on MI355X's 256 CUs.
 constexpr int64_t kResidentSplitWgs = 512;
-
-int default_tiles_per_split(int32_t num_requests, int32_t num_kv_heads, int64_t max_history) {
-  // As many splits per item as fill the GPU once (the fresh partial rides on
-  // a history workgroup, so no workgroup waits for a second round), never
-  // more than the history has steps or the merge takes.
-  const int64_t tiles = max_history > 0 ? (max_history + kTile - 1) / kTile : 0;
-  if (tiles == 0) return kWaves;
-  const int64_t steps = (tiles + kWaves - 1) / kWaves;
-  const int32_t per = requests_per_launch(num_kv_heads);
-  const int64_t items = (int64_t)(num_requests < per ? num_requests : per) * num_kv_heads;
-  int64_t s = items > 0 ? kResidentSplitWgs / items : 1;
-  s = s < 1 ? 1 : s;
-  s = s < steps ? s : steps;
-  s = s < kMaxSplits ? s : kMaxSplits;
-  const int64_t tps = (tiles + s - 1) / s;
-  return (int)(tps < kWaves ? kWaves : (tps > kMaxTilesPerSplit ? kMaxTilesPerSplit : tps));
-}
+constexpr int64_t kMaxStepsPerSplit = kMaxTilesPerSplit / kWaves;   // 64: one page-register lane per step
 
 int32_t requests_per_launch(int32_t num_kv_heads) {
   const int32_t r = kMaxInlineItems / num_kv_heads;
   return r > 0 ? r : 0;
+}
+
+// Partial slots of one launch chunk (items = requests x kv heads of the
+// chunk, one fresh-token slot each).  Explicit tiles per split: every item
+// takes the same ceil(tiles / tps) splits.  Automatic (tps = 0): per-item
+// split counts from plan_splits, at most one round of resident workgroups
+// (or one split per 64 steps of each item, when that is more) and never
+// more than the items' steps.
+int64_t partial_slots(int64_t items, int64_t max_history, int tiles_per_split) {
+  if (tiles_per_split > 0) return items * (splits_for(max_history, tiles_per_split) + 1);
+  const int64_t steps = max_history > 0 ? (max_history + kStepTok - 1) / kStepTok : 0;
+  const int64_t per64 = items * ((steps + kMaxStepsPerSplit - 1) / kMaxStepsPerSplit);
+  const int64_t bound = per64 > kResidentSplitWgs ? per64 : kResidentSplitWgs;
+  const int64_t all = items * steps;
+  return (all < bound ? all : bound) + items;
 }
 
 size_t workspace_floats(int32_t num_requests, int32_t num_kv_heads, int32_t num_heads,
@@ -1962,8 +2510,52 @@ size_t workspace_floats(int32_t num_requests, int32_t num_kv_heads, int32_t num_
   const int64_t tiles_r = (max_query_len * group + kRows - 1) / kRows;
   const int64_t per = requests_per_launch(num_kv_heads);
   const int64_t reqs = num_requests < per ? num_requests : per;     // one launch chunk
-  return (size_t)reqs * num_kv_heads * (splits_for(max_history, tiles_per_split) + 1) * tiles_r *
-         kPartialFloats;
+  return (size_t)partial_slots(reqs * num_kv_heads, max_history, tiles_per_split) * tiles_r * kPartialFloats;
+}
+
+// History splits of each item of a launch chunk (items[0 .. nitems) hold
+// qa / nq / prefix / req / kvh), their partial slots (pbase), the launch's
+// largest split count and whether each fresh partial gets a workgroup of its
+// own.  Explicit tiles per split: S = ceil(tiles / tps) for every item (at
+// most its steps).  Automatic: a common number of 128-token steps per split
+// T, the smallest that keeps the chunk's history splits within one round of
+// resident workgroups (T <= 64, one page-register lane per step), and
+// ceil(steps / T) splits per item, so that items of different lengths end
+// together.  Returns false when some item needs more than kMaxSplits splits.
+bool plan_splits(DecodeArgs& a, unsigned nitems, int64_t max_history, int tiles_per_split, int fresh) {
+  int64_t steps[kMaxInlineItems];
+  int64_t total = 0, max_steps = 0;
+  for (unsigned i = 0; i < nitems; ++i) {
+    steps[i] = a.items[i].nq > 0 ? ((int64_t)a.items[i].prefix + kStepTok - 1) / kStepTok : 0;
+    total += steps[i];
+    max_steps = steps[i] > max_steps ? steps[i] : max_steps;
+  }
+  int64_t T = 0, S = 0;
+  if (tiles_per_split > 0) {
+    S = splits_for(max_history, tiles_per_split);
+  } else {
+    T = (total + kResidentSplitWgs - 1) / kResidentSplitWgs;
+    T = T < 1 ? 1 : T;
+    for (;; ++T) {
+      int64_t n = 0;
+      for (unsigned i = 0; i < nitems; ++i) n += (steps[i] + T - 1) / T;
+      if (n <= kResidentSplitWgs || T >= kMaxStepsPerSplit) break;
+    }
+  }
+  int64_t slots = 0, max_split = 0;
+  for (unsigned i = 0; i < nitems; ++i) {
+    int64_t n = tiles_per_split > 0 ? S : (steps[i] + T - 1) / T;
+    n = n < steps[i] ? n : steps[i];
+    if (n > kMaxSplits) return false;
+    a.items[i].nsplit = (int16_t)n;
+    a.items[i].pbase = (int32_t)slots;
+    slots += n + fresh;
+    max_split = n > max_split ? n : max_split;
+  }
+  a.max_splits = (int32_t)max_split;
+  a.fresh_block = fresh && slots <= kResidentSplitWgs ? 1 : 0;
+  a.nitems = (int32_t)nitems;
+  return true;
 }
 
 // Cache, block-table and arena checks shared by both entries, then the
@@ -2018,33 +2610,46 @@ int fill_common(DecodeArgs& a, const float* q_rot, int32_t num_heads, int32_t nu
   return kOk;
 }
 
-std::atomic<uint64_t> g_split_lds_set[3] = {{0}, {0}, {0}};
+std::atomic<uint64_t> g_split_lds_set[4] = {{0}, {0}, {0}, {0}};
 
 int set_split_lds() {
-  const void* k[3] = {reinterpret_cast<const void*>(paged_decode_split_kernel<false, false>),
+  const void* k[4] = {reinterpret_cast<const void*>(paged_decode_split_kernel<false, false>),
                       reinterpret_cast<const void*>(paged_decode_split_kernel<true, false>),
-                      reinterpret_cast<const void*>(paged_decode_split_small_kernel)};
-  const size_t bytes[3] = {kLdsBytes, kLdsBytes, kSmallLdsBytes};
-  for (int i = 0; i < 3; ++i) {
+                      reinterpret_cast<const void*>(paged_decode_split_small_kernel),
+                      reinterpret_cast<const void*>(paged_decode_split_wide_kernel)};
+  const size_t bytes[4] = {kLdsBytes, kLdsBytes, kSmallLdsBytes, kWideLdsBytes};
+  for (int i = 0; i < 4; ++i) {
     const int rc = set_dynamic_lds(k[i], (int)bytes[i], g_split_lds_set[i]);
     if (rc != kOk) return rc;
   }
   return kOk;
 }
 
+// Workgroups of the launch's split grid (one per history split of each
+// item, plus one per item for the fresh partial when it has its own).
+unsigned split_workgroups(const DecodeArgs& a) {
+  int64_t n = 0;
+  for (int i = 0; i < a.nitems; ++i) n += a.items[i].nsplit + a.fresh_block;
+  return (unsigned)n;
+}
+
 // Split kernel instance of a launch chunk: the mid-step load issue when some
 // item has more 128-token steps than there are splits, with the small-row
 // score tile when no item has more than 8 rows.
 void launch_split(const DecodeArgs& a, unsigned nitems, dim3 grid, hipStream_t stream) {
-  bool multi = false, small = true;
+  bool multi = false;
+  int64_t max_rows = 0;
   for (unsigned i = 0; i < nitems; ++i) {
     if (a.items[i].nq <= 0) continue;
     const int64_t steps = ((int64_t)a.items[i].prefix + kStepTok - 1) / kStepTok;
-    if (steps > a.max_splits) multi = true;
-    if ((int64_t)a.items[i].nq * a.group > 8) small = false;
+    if (steps > a.items[i].nsplit) multi = true;
+    const int64_t r = (int64_t)a.items[i].nq * a.group;
+    max_rows = r > max_rows ? r : max_rows;
   }
-  if (small)
+  if (max_rows <= kSmRows)
     hipLaunchKernelGGL(paged_decode_split_small_kernel, grid, dim3(256), kSmallLdsBytes, stream, a);
+  else if (multi && max_rows <= kWdRows)
+    hipLaunchKernelGGL(paged_decode_split_wide_kernel, grid, dim3(256), kWideLdsBytes, stream, a);
   else if (multi)
     hipLaunchKernelGGL((paged_decode_split_kernel<true, false>), grid, dim3(256), kLdsBytes, stream, a);
   else
@@ -2098,9 +2703,8 @@ size_t oscar_paged_decode_workspace_bytes(int32_t num_requests, int32_t num_kv_h
       num_heads % num_kv_heads || max_query_len <= 0 || max_history < 0 || tiles_per_split < 0 ||
       tiles_per_split > kMaxTilesPerSplit)
     return 0;
-  const int tps = tiles_per_split > 0 ? tiles_per_split
-                                      : default_tiles_per_split(num_requests, num_kv_heads, max_history);
-  return workspace_floats(num_requests, num_kv_heads, num_heads, max_query_len, max_history, tps) * sizeof(float);
+  return workspace_floats(num_requests, num_kv_heads, num_heads, max_query_len, max_history, tiles_per_split) *
+         sizeof(float);
 }
 
 }  // extern "C"
@@ -2120,6 +2724,8 @@ struct DecodeLaunch {
   int32_t num_requests;
   int32_t max_query_len;
   int32_t num_kv_heads;
+  int64_t max_history;
+  int32_t tiles_per_split;
   bool empty;
 };
 
@@ -2156,18 +2762,18 @@ int prepare_decode(DecodeLaunch& L, const float* q_rot, const float* k_new, cons
     if (nq < 0 || nq > max_query_len || seq_lens[i] < nq || (int64_t)(seq_lens[i] - nq) > max_history)
       return kErrInvalidArgument;
   }
-  const int tps = tiles_per_split > 0 ? tiles_per_split
-                                      : default_tiles_per_split(num_requests, num_kv_heads, max_history);
-  const int64_t splits = splits_for(max_history, tps);
-  if (splits > kMaxSplits) return kErrInvalidArgument;
-  const size_t need = workspace_floats(num_requests, num_kv_heads, num_heads, max_query_len, max_history, tps) *
-                      sizeof(float);
+  if (tiles_per_split > 0 && splits_for(max_history, tiles_per_split) > kMaxSplits) return kErrInvalidArgument;
+  if (tiles_per_split == 0 && (max_history + kStepTok - 1) / kStepTok > kMaxSplits * kMaxStepsPerSplit)
+    return kErrInvalidArgument;
+  const size_t need = workspace_floats(num_requests, num_kv_heads, num_heads, max_query_len, max_history,
+                                       tiles_per_split) * sizeof(float);
   if (workspace == nullptr || workspace_size < need) return kErrWorkspaceTooSmall;
   a.k_new = k_new;
   a.v_new = v_new;
   a.win = nullptr;
   a.fresh = 1;
-  a.max_splits = (int32_t)splits;
+  L.max_history = max_history;
+  L.tiles_per_split = tiles_per_split;
   a.row_tiles = (max_query_len * a.group + kRows - 1) / kRows;
   if ((rc = set_split_lds()) != kOk) return rc;
   L.orot = orot;
@@ -2195,16 +2801,16 @@ int launch_decode(DecodeLaunch& L, hipStream_t stream) {
       const int32_t qa = L.qsl[c0 + i];
       const int32_t nq = L.qsl[c0 + i + 1] - qa;
       for (int32_t h = 0; h < L.num_kv_heads; ++h)
-        a.items[i * L.num_kv_heads + h] = ItemInfo{qa, nq, L.seqs[c0 + i] - nq, (int16_t)i, (int16_t)h};
+        a.items[i * L.num_kv_heads + h] = ItemInfo{qa, L.seqs[c0 + i] - nq, 0, (int16_t)nq, (int16_t)i, (int16_t)h, 0};
     }
     a.block_table = L.block_table ? L.block_table + (int64_t)c0 * L.bt_stride : nullptr;
     const unsigned nitems = (unsigned)(nreq * L.num_kv_heads);
-    // The fresh partial gets a workgroup of its own when one more per item
-    // still fits the resident budget, else it rides on a history split.
-    a.fresh_block = (int64_t)(a.max_splits + 1) * nitems <= kResidentSplitWgs ? 1 : 0;
-    const int gx = a.max_splits + a.fresh_block;
-    dim3 grid((unsigned)(gx > 0 ? gx : 1), nitems, (unsigned)a.row_tiles);
-    launch_split(a, nitems, grid, stream);
+    // Per-item splits; the fresh partial gets a workgroup of its own when one
+    // more per item still fits the resident budget, else it rides on a
+    // history split.
+    if (!plan_splits(a, nitems, L.max_history, L.tiles_per_split, 1)) return kErrInvalidArgument;
+    const unsigned gx = split_workgroups(a);
+    if (gx > 0) launch_split(a, nitems, dim3(gx, 1, (unsigned)a.row_tiles), stream);
     if (hipGetLastError() != hipSuccess) return kErrLaunch;
     const int rc = launch_merge(a, (int64_t)L.max_query_len * a.group, nitems, L.orot, stream);
     if (rc != kOk) return rc;
@@ -2378,12 +2984,11 @@ int oscar_decode_only(const float* q_rot, int32_t num_heads, int32_t num_kv_head
   if (!seq_lens) return kErrInvalidArgument;
   for (int32_t i = 0; i < num_requests; ++i)
     if (seq_lens[i] < 0 || seq_lens[i] > max_history) return kErrInvalidArgument;
-  const int tps = tiles_per_split > 0 ? tiles_per_split
-                                      : default_tiles_per_split(num_requests, num_kv_heads, max_history);
-  const int64_t splits = splits_for(max_history, tps);
-  if (splits > kMaxSplits) return kErrInvalidArgument;
-  const size_t partials = workspace_floats(num_requests, num_kv_heads, num_heads, 1, max_history, tps) *
-                          sizeof(float);
+  if (tiles_per_split > 0 && splits_for(max_history, tiles_per_split) > kMaxSplits) return kErrInvalidArgument;
+  if (tiles_per_split == 0 && (max_history + kStepTok - 1) / kStepTok > kMaxSplits * kMaxStepsPerSplit)
+    return kErrInvalidArgument;
+  const size_t partials = workspace_floats(num_requests, num_kv_heads, num_heads, 1, max_history,
+                                           tiles_per_split) * sizeof(float);
   const int32_t per = requests_per_launch(num_kv_heads);
   const size_t need = bounds_offset(partials) +
                       (size_t)(num_requests < per ? num_requests : per) * 2 * sizeof(int32_t);
@@ -2395,24 +3000,24 @@ int oscar_decode_only(const float* q_rot, int32_t num_heads, int32_t num_kv_head
   a.v_new = nullptr;
   a.win = window ? bounds : nullptr;
   a.fresh = 0;
-  a.max_splits = (int32_t)splits;
   a.row_tiles = (a.group + kRows - 1) / kRows;
   if ((rc = set_split_lds()) != kOk) return rc;
   for (int32_t c0 = 0; c0 < num_requests; c0 += per) {
     const int32_t nreq = num_requests - c0 < per ? num_requests - c0 : per;
     for (int32_t i = 0; i < nreq; ++i)
       for (int32_t h = 0; h < num_kv_heads; ++h)
-        a.items[i * num_kv_heads + h] = ItemInfo{c0 + i, 1, seq_lens[c0 + i], (int16_t)i, (int16_t)h};
+        a.items[i * num_kv_heads + h] = ItemInfo{c0 + i, seq_lens[c0 + i], 0, 1, (int16_t)i, (int16_t)h, 0};
     a.block_table = block_table ? block_table + (int64_t)c0 * block_table_stride : nullptr;
     const unsigned nitems = (unsigned)(nreq * num_kv_heads);
+    if (!plan_splits(a, nitems, max_history, tiles_per_split, 0)) return kErrInvalidArgument;
     if (window) {
       hipLaunchKernelGGL(decode_only_bounds_kernel, dim3((unsigned)nreq), dim3(kBoundsThreads), 0, stream, a, bounds,
                          sink_eff, recent_tokens);
       if (hipGetLastError() != hipSuccess) return kErrLaunch;
     }
-    if (a.max_splits > 0) {
-      dim3 grid((unsigned)a.max_splits, nitems, (unsigned)a.row_tiles);
-      launch_split(a, nitems, grid, stream);
+    const unsigned gx = split_workgroups(a);
+    if (gx > 0) {
+      launch_split(a, nitems, dim3(gx, 1, (unsigned)a.row_tiles), stream);
       if (hipGetLastError() != hipSuccess) return kErrLaunch;
     }
     if ((rc = launch_merge(a, a.group, nitems, OutRotation{nullptr, nullptr, 0, 0}, stream)) != kOk) return rc;

@@ -63,34 +63,59 @@ DECODE_MAX_TILES_PER_SPLIT = 256
 
 
 DECODE_RESIDENT_SPLITS = 512          # split workgroups resident at once (two per CU, 256 CUs)
+DECODE_STEP = 128                      # history tokens per decode step (4 tiles)
+DECODE_MAX_STEPS_PER_SPLIT = 64
 
 
-def decode_tiles_per_split(max_requests: int, num_kv_heads: int, max_history: int) -> int:
-    """The library's default split length (in tiles) for this batch shape:
-    as many splits per item as fill the GPU once, at most one per 4-tile
-    step and at most DECODE_MAX_SPLITS."""
-    tiles = -(-max_history // DECODE_TILE) if max_history > 0 else 0
-    if tiles == 0:
-        return 4
-    steps = -(-tiles // 4)
-    items = min(max_requests, DECODE_LAUNCH_ITEMS // num_kv_heads) * num_kv_heads
-    s = max(DECODE_RESIDENT_SPLITS // items, 1) if items > 0 else 1
-    s = min(s, steps, DECODE_MAX_SPLITS)
-    return min(max(-(-tiles // s), 4), DECODE_MAX_TILES_PER_SPLIT)
+def decode_partial_slots(items: int, max_history: int, tiles_per_split: int = 0) -> int:
+    """Partial slots of one launch chunk of `items` (request, kv head) items,
+    one fresh-token slot each.  Explicit tiles per split: ceil(tiles / tps)
+    splits per item.  Automatic: per-item split counts that keep the chunk
+    within one round of resident workgroups (or one split per 64 steps of
+    each item when that is more), never more than the items' steps."""
+    if tiles_per_split:
+        tiles = -(-max_history // DECODE_TILE) if max_history > 0 else 0
+        return items * (-(-tiles // tiles_per_split) + 1)
+    steps = -(-max_history // DECODE_STEP) if max_history > 0 else 0
+    bound = max(items * -(-steps // DECODE_MAX_STEPS_PER_SPLIT), DECODE_RESIDENT_SPLITS)
+    return min(items * steps, bound) + items
+
+
+def decode_split_plan(query_lens, histories, max_history: int, tiles_per_split: int = 0, fresh: int = 1):
+    """The library's per-item history splits of one launch chunk (items in
+    order, one per (request, kv head)): returns (nsplit, pbase) lists.
+    Explicit tiles per split: ceil(tiles / tps) splits per item.  Automatic:
+    the smallest common number T of 128-token steps per split (T <= 64) that
+    keeps the history splits within one round of resident workgroups, and
+    ceil(steps / T) splits per item; never more splits than steps."""
+    steps = [-(-h // DECODE_STEP) if q > 0 and h > 0 else 0 for q, h in zip(query_lens, histories)]
+    if tiles_per_split:
+        tiles = -(-max_history // DECODE_TILE) if max_history > 0 else 0
+        per = [-(-tiles // tiles_per_split)] * len(steps)
+    else:
+        T = max(1, -(-sum(steps) // DECODE_RESIDENT_SPLITS))
+        while sum(-(-n // T) for n in steps) > DECODE_RESIDENT_SPLITS and T < DECODE_MAX_STEPS_PER_SPLIT:
+            T += 1
+        per = [-(-n // T) for n in steps]
+    nsplit, pbase, slot = [], [], 0
+    for n, st in zip(per, steps):
+        n = min(n, st)
+        nsplit.append(n)
+        pbase.append(slot)
+        slot += n + fresh
+    return nsplit, pbase
 
 
 def decode_workspace_bytes(max_requests: int, num_kv_heads: int, num_heads: int, max_query_len: int,
                            max_history: int, tiles_per_split: int = 0) -> int:
     """Same value as oscar_paged_decode_workspace_bytes (no library needed):
-    one fp32 partial (32 rows x 256 + max + sum) per (request, kv head,
-    history split or the fresh-token split, row tile)."""
-    tps = tiles_per_split or decode_tiles_per_split(max_requests, num_kv_heads, max_history)
-    tiles = -(-max_history // DECODE_TILE) if max_history > 0 else 0
-    splits = -(-tiles // tps)
+    one fp32 partial (32 rows x 256 + max + sum) per partial slot and row tile
+    of one launch chunk (requests of a launch share one workspace)."""
     row_tiles = -(-(max_query_len * (num_heads // num_kv_heads)) // DECODE_ROWS)
-    per_launch = DECODE_LAUNCH_ITEMS // num_kv_heads         # requests per launch share one workspace
+    per_launch = DECODE_LAUNCH_ITEMS // num_kv_heads
     chunk = min(max_requests, per_launch)
-    return chunk * num_kv_heads * (splits + 1) * row_tiles * DECODE_PARTIAL_FLOATS * 4
+    return decode_partial_slots(chunk * num_kv_heads, max_history, tiles_per_split) * row_tiles * \
+        DECODE_PARTIAL_FLOATS * 4
 
 
 def kv_block_bytes(block_size: int, num_kv_heads: int, slot_width: int, layers: int) -> int:
