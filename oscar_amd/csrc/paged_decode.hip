@@ -435,15 +435,7 @@ __device__ __forceinline__ float half_wave_reduce(float x) {
 // (long-history MTP reads such as 1 x 4 tokens over 24K) run the first
 // instance, whose allocation was tuned for their window tiles; multi-step
 // launches run the second (C3 55.1 -> 54.1 us; C5 unchanged within noise).
-// kSmall: every item of the launch has at most 8 rows (single-token requests
-// of a GQA group of 1..8, or two tokens of a group of 4): the score tile is
-// computed as S = Q K^T instead, so a lane holds one token and 16 rows of
-// which registers 0..3 (rows 4g .. 4g + 3) are the rows' high-part products
-// and registers 4..7 their low-part products (rows 8 .. 15 of the Q operand
-// hold the low parts, which halves the score MFMAs), and the softmax runs on
-// 4 values per lane (with half-wave reductions over tokens) instead of on 16
-// mostly padded ones.
-template <bool kMidIssue, bool kSmall>
+template <bool kMidIssue>
 __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
   // History splits are dispatched as 0, S - 1, S - 2, ..., 1: the first and
@@ -585,12 +577,6 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   floatx16 acc[2] = {floatx16{}, floatx16{}};   // O^T of features 64w .. 64w + 63 (2 blocks of 32)
   float m_run = -__builtin_inff();
   float l_run = 0.f, z_run = 0.f, ps_run = 0.f;  // this lane's share of its row's sums (own tiles)
-  // kSmall: running maxima and this lane's (token's) shares of the sums of
-  // rows 4g .. 4g + 3, and those rows' q sums.
-  float m4[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
-  float l4[4] = {0.f, 0.f, 0.f, 0.f}, z4[4] = {0.f, 0.f, 0.f, 0.f}, ps4[4] = {0.f, 0.f, 0.f, 0.f};
-  floatx4 qs4 = floatx4{0.f, 0.f, 0.f, 0.f};
-  if constexpr (kSmall) qs4 = *reinterpret_cast<const floatx4*>(&S.qsum[4 * g]);
   const float qsum = S.qsum[col];
   const uint32_t ones16 = magic_ones();
   // PV operand lane constants: block b, row m = col is code sp = 2b + (m & 1)
@@ -633,9 +619,6 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
 
     // ---- own tile: token parameters and byte-transposed V codes ----
     bool big;
-    // kSmall: this lane's token's parameters stay in registers
-    float t_a = 0.f, t_b = 0.f, t_m = 0.f, t_vs = 0.f, t_rv = 0.f, t_vz = 0.f;
-    bool t_win = false;
     {
       const bool win = (wmw >> col) & 1u;
       const bool used = col < nvalid && !win;
@@ -643,15 +626,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
       const float kz = f16_bits_to_f32(L.meta[0] >> 16);
       const float vsc = f16_bits_to_f32(L.meta[1]);
       const float vz = f16_bits_to_f32(L.meta[1] >> 16);
-      if constexpr (kSmall) {
-        t_a = used ? 4.f * ksc * a.scale_log2 : (win ? a.scale_log2 : 0.f);
-        t_b = used ? (kz - 4.f * ksc) * a.scale_log2 : 0.f;
-        t_m = (used || win) ? 0.f : -__builtin_inff();
-        t_rv = used ? 1.f / vsc : 0.f;
-        t_vs = used ? vsc : 0.f;
-        t_vz = used ? vz * t_rv : 0.f;
-        t_win = win;
-      } else if (g == 0) {
+      if (g == 0) {
         S.ta[w][col] = used ? 4.f * ksc * a.scale_log2 : (win ? a.scale_log2 : 0.f);
         S.tb[w][col] = used ? (kz - 4.f * ksc) * a.scale_log2 : 0.f;
         S.tm[w][col] = (used || win) ? 0.f : -__builtin_inff();
@@ -679,47 +654,29 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
       // Q^T operands (high and low parts, so the products see q to 2^-22;
       // the code operands 1 + c/4 are exact) are read from LDS one k-step
       // pair ahead of their use.
-      // kSmall: rows 8 .. 15 of the Q operand are the low parts of rows
-      // 0 .. 7, so one MFMA pass gives both products (row r: high part,
-      // row 8 + r: low part; the fixup adds them).
-      const half8* qsrc = reinterpret_cast<const half8*>(
-          (kSmall && (col & 24) == 8) ? &S.qlo[(g * kRows + col - 8) * 8]
-                                      : &S.q[(g * kRows + col) * 8]);   // + m * 2 * kRows
+      const half8* qsrc = reinterpret_cast<const half8*>(&S.q[(g * kRows + col) * 8]);   // + m * 2 * kRows
       const half8* qlsrc = reinterpret_cast<const half8*>(&S.qlo[(g * kRows + col) * 8]);
       const uint32_t kw[8] = {L.kc0[0], L.kc0[1], L.kc0[2], L.kc0[3], L.kc1[0], L.kc1[1], L.kc1[2], L.kc1[3]};
       // One accumulator chain: the other workgroup on the SIMD covers the
       // MFMA latency.
       s = floatx16{};
-      // S^T = K Q^T (lane: row col, 16 tokens), or S = Q K^T in the kSmall
-      // instance (lane: token col, rows 8 (r / 4) + 4g + r % 4): the same
-      // operand registers either way.
+      // S^T = K Q^T (lane: row col, 16 tokens)
       auto score_mfma = [&](const half8& kop, const half8& qop) {
-        if constexpr (kSmall)
-          s = __builtin_amdgcn_mfma_f32_32x32x16_f16(qop, kop, s, 0, 0, 0);
-        else
-          s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qop, s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qop, s, 0, 0, 0);
       };
-      half8 qa = qsrc[0], qb = qsrc[2 * kRows], qal{}, qbl{};
-      if constexpr (!kSmall) {
-        qal = qlsrc[0];
-        qbl = qlsrc[2 * kRows];
-      }
+      half8 qa = qsrc[0], qb = qsrc[2 * kRows], qal = qlsrc[0], qbl = qlsrc[2 * kRows];
       auto qk_pair = [&](int j, const half8& k0, const half8& k1) {
         half8 na = qa, nb = qb, nal = qal, nbl = qbl;
         if (j < 7) {
           na = qsrc[(2 * j + 2) * 2 * kRows];
           nb = qsrc[(2 * j + 3) * 2 * kRows];
-          if constexpr (!kSmall) {
-            nal = qlsrc[(2 * j + 2) * 2 * kRows];
-            nbl = qlsrc[(2 * j + 3) * 2 * kRows];
-          }
+          nal = qlsrc[(2 * j + 2) * 2 * kRows];
+          nbl = qlsrc[(2 * j + 3) * 2 * kRows];
         }
         score_mfma(k0, qa);
         score_mfma(k1, qb);
-        if constexpr (!kSmall) {
-          score_mfma(k0, qal);
-          score_mfma(k1, qbl);
-        }
+        score_mfma(k0, qal);
+        score_mfma(k1, qbl);
         qa = na;
         qb = nb;
         qal = nal;
@@ -755,7 +712,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
         }
         // window tokens (the other lanes hold zeros): low part of k against
         // the high part of q (the low-low product is below 2^-22 of the
-        // score's terms; kSmall rows 8 .. 15 take it, harmlessly)
+        // score's terms)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const half8 la = __builtin_bit_cast(half8, im[2 * j]);
@@ -785,44 +742,28 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
       }
     }
     issue_next();
-    if constexpr (kSmall) {
-      // scores of rows 4g + i (i < 4) against this lane's token; row maxima
-      // over the tile's 32 tokens (the half wave)
-      floatx4 mb4;
+    // scores (lane: row col, tokens 8 (r / 4) + 4g + r % 4) and the tile's row max
+    float mb = -__builtin_inff();
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const floatx4 av = *reinterpret_cast<const floatx4*>(&S.ta[w][8 * jj + 4 * g]);
+      const floatx4 bv = *reinterpret_cast<const floatx4*>(&S.tb[w][8 * jj + 4 * g]);
+      const floatx4 tmv = *reinterpret_cast<const floatx4*>(&S.tm[w][8 * jj + 4 * g]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        s[i] = fmaf(t_a, s[i] + s[4 + i], t_b * qs4[i]) + t_m;
-        mb4[i] = half_wave_reduce<true>(s[i]);
+        s[4 * jj + i] = fmaf(av[i], s[4 * jj + i], bv[i] * qsum) + tmv[i];
+        mb = fmaxf(mb, s[4 * jj + i]);
       }
-      if (col == 0) *reinterpret_cast<floatx4*>(&S.mx[w][4 * g]) = mb4;
-    } else {
-      // scores (lane: row col, tokens 8 (r / 4) + 4g + r % 4) and the tile's row max
-      float mb = -__builtin_inff();
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const floatx4 av = *reinterpret_cast<const floatx4*>(&S.ta[w][8 * jj + 4 * g]);
-        const floatx4 bv = *reinterpret_cast<const floatx4*>(&S.tb[w][8 * jj + 4 * g]);
-        const floatx4 tmv = *reinterpret_cast<const floatx4*>(&S.tm[w][8 * jj + 4 * g]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          s[4 * jj + i] = fmaf(av[i], s[4 * jj + i], bv[i] * qsum) + tmv[i];
-          mb = fmaxf(mb, s[4 * jj + i]);
-        }
-      }
-      mb = fmaxf(mb, shfl_xor_f32(mb, 32));
-      if (g == 0) S.mx[w][col] = mb;
     }
+    mb = fmaxf(mb, shfl_xor_f32(mb, 32));
+    if (g == 0) S.mx[w][col] = mb;
     if (lane == 0) S.big[w] = big ? 1u : 0u;
     lds_barrier();
 
     // ---- common max of the step (same decision in every wave), P' of the own tile ----
     const bool eager = (S.big[0] | S.big[1] | S.big[2] | S.big[3]) != 0u;
     {
-      // (kSmall: rows 8 and up of the row maxima are not written; those O^T
-      // columns are never stored)
-      const float M = (kSmall && col >= 8)
-                          ? -__builtin_inff()
-                          : fmaxf(fmaxf(S.mx[0][col], S.mx[1][col]), fmaxf(S.mx[2][col], S.mx[3][col]));
+      const float M = fmaxf(fmaxf(S.mx[0][col], S.mx[1][col]), fmaxf(S.mx[2][col], S.mx[3][col]));
       const bool need = M > m_run + (eager ? 0.f : kLazy);
       const bool resc = need && m_run != -__builtin_inff();
       if (__ballot(resc)) {
@@ -835,89 +776,51 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
       }
       if (need) m_run = M;
     }
-    if constexpr (kSmall) {
-      // Rows 4g + i: the same decisions on the same maxima, then P' of this
-      // lane's token for each row into its slot of the row (slots 4u + v
-      // hold tokens 4u + (0, 2, 1, 3)[v]), and the token's shares of the
-      // row sums over the weights as the PV pass sees them.
-      floatx4 M4 = *reinterpret_cast<const floatx4*>(&S.mx[0][4 * g]);
+    // exp2(-inf - m) = 0 needs a finite m: rows that have seen no key yet use 0.
+    const float m_use = m_run == -__builtin_inff() ? 0.f : m_run;
+    float psum = 0.f, zsum = 0.f, pss = 0.f;
+    const half2v ones{(_Float16)1.f, (_Float16)1.f};
+    _Float16* prow = &S.p[w][col * kPRow + 4 * g];
+    _Float16* pwrow = &S.pw[w][col * kPRow + 4 * g];
 #pragma unroll
-      for (int ww = 1; ww < kWaves; ++ww) {
-        const floatx4 x = *reinterpret_cast<const floatx4*>(&S.mx[ww][4 * g]);
+    // The row sums take each token's weight as the PV pass sees it (after
+    // its fp16 rounding: P' / vs of an INT2 token, 4 * (p / 4) of a window
+    // token), so that the output is a convex combination of the values
+    // whatever that rounding did.
+    for (int jj = 0; jj < 4; ++jj) {
+      const floatx4 vsv = *reinterpret_cast<const floatx4*>(&S.tvs[w][8 * jj + 4 * g]);
+      const floatx4 rvv = *reinterpret_cast<const floatx4*>(&S.trv[w][8 * jj + 4 * g]);
+      const floatx4 zrv = *reinterpret_cast<const floatx4*>(&S.tvz[w][8 * jj + 4 * g]);
+      float p[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) M4[i] = fmaxf(M4[i], x[i]);
-      }
-      const int slot = (col & ~3) | ((col & 1) << 1) | ((col >> 1) & 1);
+      for (int i = 0; i < 4; ++i) p[i] = exp2_raw(s[4 * jj + i] - m_use);
+      // slots 8jj + 4g + {0, 1, 2, 3} hold tokens 8jj + 4g + {0, 2, 1, 3}
+      const half4 h = half4{(_Float16)(p[0] * vsv[0]), (_Float16)(p[2] * vsv[2]), (_Float16)(p[1] * vsv[1]),
+                            (_Float16)(p[3] * vsv[3])};
+      *reinterpret_cast<half4*>(prow + 8 * jj) = h;
+      pss = __builtin_amdgcn_fdot2(half2v{h[0], h[1]}, ones, pss, false);
+      pss = __builtin_amdgcn_fdot2(half2v{h[2], h[3]}, ones, pss, false);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const bool need = M4[i] > m4[i] + (eager ? 0.f : kLazy);
-        const bool resc = need && m4[i] != -__builtin_inff();
-        const float alpha = resc ? exp2_raw(m4[i] - M4[i]) : 1.f;
-        l4[i] *= alpha;
-        z4[i] *= alpha;
-        ps4[i] *= alpha;
-        if (need) m4[i] = M4[i];
-        const float m_use = m4[i] == -__builtin_inff() ? 0.f : m4[i];
-        const float pr = exp2_raw(s[i] - m_use);
-        const _Float16 h = (_Float16)(pr * t_vs);
-        S.p[w][(4 * g + i) * kPRow + slot] = h;
-        const float wh = (float)h;
-        ps4[i] += wh;
-        l4[i] = fmaf(wh, t_rv, l4[i]);
-        z4[i] = fmaf(wh, t_vz, z4[i]);
-        if (wmw != 0u) {
-          const _Float16 hw = t_win ? (_Float16)(0.25f * pr) : (_Float16)0.f;
-          S.pw[w][(4 * g + i) * kPRow + slot] = hw;
-          l4[i] = fmaf(4.f, (float)hw, l4[i]);
-        }
+        const float wi = (float)h[i == 1 ? 2 : (i == 2 ? 1 : i)];
+        psum = fmaf(wi, rvv[i], psum);
+        zsum = fmaf(wi, zrv[i], zsum);
       }
-    } else {
-      // exp2(-inf - m) = 0 needs a finite m: rows that have seen no key yet use 0.
-      const float m_use = m_run == -__builtin_inff() ? 0.f : m_run;
-      float psum = 0.f, zsum = 0.f, pss = 0.f;
-      const half2v ones{(_Float16)1.f, (_Float16)1.f};
-      _Float16* prow = &S.p[w][col * kPRow + 4 * g];
-      _Float16* pwrow = &S.pw[w][col * kPRow + 4 * g];
-#pragma unroll
-      // The row sums take each token's weight as the PV pass sees it (after
-      // its fp16 rounding: P' / vs of an INT2 token, 4 * (p / 4) of a window
-      // token), so that the output is a convex combination of the values
-      // whatever that rounding did.
-      for (int jj = 0; jj < 4; ++jj) {
-        const floatx4 vsv = *reinterpret_cast<const floatx4*>(&S.tvs[w][8 * jj + 4 * g]);
-        const floatx4 rvv = *reinterpret_cast<const floatx4*>(&S.trv[w][8 * jj + 4 * g]);
-        const floatx4 zrv = *reinterpret_cast<const floatx4*>(&S.tvz[w][8 * jj + 4 * g]);
-        float p[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) p[i] = exp2_raw(s[4 * jj + i] - m_use);
-        // slots 8jj + 4g + {0, 1, 2, 3} hold tokens 8jj + 4g + {0, 2, 1, 3}
-        const half4 h = half4{(_Float16)(p[0] * vsv[0]), (_Float16)(p[2] * vsv[2]), (_Float16)(p[1] * vsv[1]),
-                              (_Float16)(p[3] * vsv[3])};
-        *reinterpret_cast<half4*>(prow + 8 * jj) = h;
-        pss = __builtin_amdgcn_fdot2(half2v{h[0], h[1]}, ones, pss, false);
-        pss = __builtin_amdgcn_fdot2(half2v{h[2], h[3]}, ones, pss, false);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float wi = (float)h[i == 1 ? 2 : (i == 2 ? 1 : i)];
-          psum = fmaf(wi, rvv[i], psum);
-          zsum = fmaf(wi, zrv[i], zsum);
-        }
-        if (wmw != 0u) {
-          const uint32_t wb = wmw >> (8 * jj + 4 * g);
-          const half4 hw = half4{(wb & 1u) ? (_Float16)(0.25f * p[0]) : (_Float16)0.f,
-                                 (wb & 4u) ? (_Float16)(0.25f * p[2]) : (_Float16)0.f,
-                                 (wb & 2u) ? (_Float16)(0.25f * p[1]) : (_Float16)0.f,
-                                 (wb & 8u) ? (_Float16)(0.25f * p[3]) : (_Float16)0.f};
-          *reinterpret_cast<half4*>(pwrow + 8 * jj) = hw;
-          float ws = __builtin_amdgcn_fdot2(half2v{hw[0], hw[1]}, ones, 0.f, false);
-          ws = __builtin_amdgcn_fdot2(half2v{hw[2], hw[3]}, ones, ws, false);
-          psum = fmaf(4.f, ws, psum);
-        }
+      if (wmw != 0u) {
+        const uint32_t wb = wmw >> (8 * jj + 4 * g);
+        const half4 hw = half4{(wb & 1u) ? (_Float16)(0.25f * p[0]) : (_Float16)0.f,
+                               (wb & 4u) ? (_Float16)(0.25f * p[2]) : (_Float16)0.f,
+                               (wb & 2u) ? (_Float16)(0.25f * p[1]) : (_Float16)0.f,
+                               (wb & 8u) ? (_Float16)(0.25f * p[3]) : (_Float16)0.f};
+        *reinterpret_cast<half4*>(pwrow + 8 * jj) = hw;
+        float ws = __builtin_amdgcn_fdot2(half2v{hw[0], hw[1]}, ones, 0.f, false);
+        ws = __builtin_amdgcn_fdot2(half2v{hw[2], hw[3]}, ones, ws, false);
+        psum = fmaf(4.f, ws, psum);
       }
-      l_run += psum;
-      z_run += zsum;
-      ps_run += pss;
     }
+    l_run += psum;
+    z_run += zsum;
+    ps_run += pss;
     lds_barrier();
 
     // ---- O^T (features 64w .. 64w + 63) += V^T P'^T over the step's tiles ----
@@ -980,28 +883,13 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   // step's scores (every wave has passed that step's barriers by now).
   float* red = reinterpret_cast<float*>(S.q);
   static_assert(sizeof(S.q) >= kWaves * 3 * kRows * sizeof(float), "row sums fit the Q^T area");
-  if constexpr (kSmall) {
-    // rows 4g + i: sums over the half wave's tokens
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float lt = half_wave_reduce<false>(l4[i]);
-      const float zt = half_wave_reduce<false>(z4[i]);
-      const float pt = half_wave_reduce<false>(ps4[i]);
-      if (col == 0) {
-        red[(w * 3 + 0) * kRows + 4 * g + i] = lt;
-        red[(w * 3 + 1) * kRows + 4 * g + i] = zt;
-        red[(w * 3 + 2) * kRows + 4 * g + i] = pt;
-      }
-    }
-  } else {
-    l_run += shfl_xor_f32(l_run, 32);
-    z_run += shfl_xor_f32(z_run, 32);
-    ps_run += shfl_xor_f32(ps_run, 32);
-    if (g == 0) {
-      red[(w * 3 + 0) * kRows + col] = l_run;
-      red[(w * 3 + 1) * kRows + col] = z_run;
-      red[(w * 3 + 2) * kRows + col] = ps_run;
-    }
+  l_run += shfl_xor_f32(l_run, 32);
+  z_run += shfl_xor_f32(z_run, 32);
+  ps_run += shfl_xor_f32(ps_run, 32);
+  if (g == 0) {
+    red[(w * 3 + 0) * kRows + col] = l_run;
+    red[(w * 3 + 1) * kRows + col] = z_run;
+    red[(w * 3 + 2) * kRows + col] = ps_run;
   }
   lds_barrier();
   float lt = 0.f, zt = 0.f, pt = 0.f;
@@ -1581,533 +1469,6 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(Decode
   }
 }
 
-// ---------------------------------------------------------------- wide split kernel
-// Multi-step launches whose items have 9 to 24 rows (MTP steps of a few
-// tokens over a GQA group, e.g. 4 tokens x 6 heads): the small-row kernel's
-// structure (each wavefront walks its own 32-token tiles with its own
-// running maxima and sums, a per-wavefront LDS ring of tiles filled by
-// buffer loads to LDS, window tokens in a pass of their own after the loop)
-// on v_mfma_f32_32x32x16_f16 tiles of 32 tokens x 32 rows.  Lane l = (j, g),
-// j = l % 32, g = l / 32:
-//  * S^T = K Q^T: A = K: lane (t, g) holds token pi(t) (pi swaps bits 2 and 3
-//    of t) with the features of window-image block m, half g; B = Q^T (high
-//    part, then low part, from LDS).  Result register r of lane (j, g) is the
-//    score of token 16 (r >> 3) + 8g + 4 ((r >> 2) & 1) + (r & 3) for row j,
-//    so that lane group g holds tokens 8g .. 8g + 7 of each 16-token k-step
-//    of the PV pass, exactly the token grouping of the window V image.
-//  * O^T += V^T P'^T: A = V^T: lane (m, g) holds feature 64q + 4 (m >> 1) + 2b
-//    + (m & 1) of tokens 16s + 8g + {0, 2, 1, 3, 4, 6, 5, 7} (k-step s), B =
-//    P'^T in the same order straight from the score registers.  Output
-//    registers 4jq + 2h + e of blocks (q, b) are features 64q + 16jq + 8g + 4h
-//    + 2b + e of row j: the whole 256 features x 32 rows in 128 registers.
-constexpr int kWdRows = 24;
-constexpr int kWdRing = 2;       // tiles resident per wavefront: the one computed and one in flight
-
-struct WideLds {
-  _Float16 q[16 * 2 * kWdRows * 8];        // Q^T operand [m][g][row][8], fp16 high part
-  _Float16 qlo[16 * 2 * kWdRows * 8];      // low part fp16(q - high)
-  float qsum[kWdRows];
-  SmallTileLds tile[kWaves];
-  uint32_t wbits[kWaves][kMaxTilesPerSplit / kWaves];
-  SmallSlot ring[kWaves][kWdRing];
-};
-
-struct WideCombineLds {
-  float o[2][kWdRows][kHeadDim];           // two wavefronts' scaled rows
-  float m[kWaves][kRows];
-  float l[kWaves][kRows];
-};
-
-constexpr size_t kWideLdsBytes = sizeof(WideLds) > sizeof(WideCombineLds)
-                                     ? (sizeof(WideLds) > sizeof(FreshLds) ? sizeof(WideLds) : sizeof(FreshLds))
-                                     : (sizeof(WideCombineLds) > sizeof(FreshLds) ? sizeof(WideCombineLds)
-                                                                                  : sizeof(FreshLds));
-static_assert(kWideLdsBytes <= 80 * 1024, "two workgroups' LDS must fit the CU's 160 KiB");
-
-__device__ __forceinline__ int swap23(int t) { return (t & ~12) | ((t & 4) << 1) | ((t & 8) >> 1); }
-
-// The wide kernel's tile loads: as load_small_tile, with lane (t, g) copying
-// the 32 K code bytes 32g .. 32g + 31 of token pi(t) in two 16-byte loads.
-__device__ __forceinline__ void load_wide_tile(const DecodeArgs& a, SmallSlot& slot, int page, int p0, int prefix,
-                                               int kvh, int lane) {
-  const int t = lane & 31, g = lane >> 5;
-  const bool tile_ok = p0 < prefix && page >= 0;
-  const int pgc = tile_ok ? page : 0;
-  const int prow0 = (int)fast_mod((uint32_t)p0, a.bs_div);
-  const int nrow = tile_ok ? min(kTile, prefix - p0) : 0;
-  auto row_of = [&](int tk) { return tk < nrow ? prow0 + tk : 0; };
-  const uint32_t krec = (uint32_t)((int64_t)(a.block_size - 1) * a.k_tok + kKCodeOff + kCodeBytes);
-  const uint32_t vrec = (uint32_t)((int64_t)(a.block_size - 1) * a.v_tok + kCodeBytes);
-  const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(a.k_cache + (int64_t)pgc * a.k_page + (int64_t)kvh * a.k_head), (short)0, krec, 0x00020000);
-  const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(a.v_cache + (int64_t)pgc * a.v_page + (int64_t)kvh * a.v_head), (short)0, vrec, 0x00020000);
-  const int krow = row_of(swap23(t)) * (int)a.k_tok + kKCodeOff + 32 * g;
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void*)&slot.kc[h][0], 16, krow + 16 * h, 0, 0, 0);
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int tk = 16 * i + (lane >> 2);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_void*)&slot.vc[16 * i][0], 16,
-                                             row_of(tk) * (int)a.v_tok + 16 * (lane & 3), 0, 0, 0);
-  }
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void*)&slot.meta[0], 4,
-                                           row_of(lane >> 1) * (int)a.k_tok + 4 * (lane & 1), 0, 0, 0);
-  const bool arena = a.stage_rows > 0;
-  const int64_t seat0 = arena ? (int64_t)fast_mod((uint32_t)pgc, a.rows_div) * a.block_size + prow0 : 0;
-  const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc(
-      arena ? (void*)(a.owner + seat0) : (void*)a.k_cache, (short)0, arena ? (uint32_t)(kTile * 8) : 0u,
-      0x00020000);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(orr, (lds_void*)&slot.own[0], 4, 4 * lane, 0, 0, 0);
-}
-
-__device__ __forceinline__ float xor32_max(float x) {
-  const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
-  return fmaxf(__int_as_float(s32[0]), __int_as_float(s32[1]));
-}
-__device__ __forceinline__ float xor32_sum(float x) {
-  const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
-  return __int_as_float(s32[0]) + __int_as_float(s32[1]);
-}
-
-__global__ __launch_bounds__(256, 2) void paged_decode_split_wide_kernel(DecodeArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
-  int bx;
-  const int item = locate_item(a, (int)blockIdx.x, bx);
-  const ItemInfo it = a.items[item];
-  const int rows = it.nq * a.group;
-  if (it.nq <= 0 || blockIdx.z != 0) return;
-  if (bx >= it.nsplit) {                  // the fresh-token workgroup, or none for this item
-    if (a.fresh_block && bx == it.nsplit)
-      fresh_partial(a, it, item, 0, *reinterpret_cast<FreshLds*>(smem_raw), (int)threadIdx.x);
-    return;
-  }
-  const int split = bx == 0 ? 0 : it.nsplit - bx;
-  const int prefix = it.prefix;
-  const int steps = (prefix + kStepTok - 1) / kStepTok;
-  const int rem = steps % it.nsplit;
-  const int fresh_split = steps < it.nsplit ? steps : (rem != 0 ? it.nsplit - 1 : it.nsplit / 2);
-  const bool fresh_here = a.fresh && !a.fresh_block && split == fresh_split;
-  if (split >= steps) {
-    if (fresh_here) fresh_partial(a, it, item, 0, *reinterpret_cast<FreshLds*>(smem_raw), (int)threadIdx.x);
-    return;
-  }
-  WideLds& S = *reinterpret_cast<WideLds*>(smem_raw);
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int j = lane & 31, g = lane >> 5;
-  const int kvh = it.kvh;
-  const int nsplit = it.nsplit;
-  const int nst = (steps - 1 - split) / nsplit + 1;
-  const bool arena = a.stage_rows > 0;
-  int win_head = 0, win_tail = 0;
-  if (a.win) {
-    typedef __attribute__((address_space(4))) const int32_t const_i32;
-    const const_i32* wb = (const const_i32*)a.win;
-    win_head = wb[2 * it.req];
-    win_tail = wb[2 * it.req + 1];
-  }
-
-  // ---- requests before any wait: the query features (thread: row r8,
-  // features 32 c8 .. + 31) and the wavefront's page of each step ----
-  const int r8 = tid >> 3, c8 = tid & 7;
-  floatx4 x[8];
-  {
-    const int row = r8 < rows ? r8 : rows - 1;
-    const int jq = row / a.group, h = kvh * a.group + (row - jq * a.group);
-    const floatx4* src = reinterpret_cast<const floatx4*>(a.q + ((int64_t)(it.qa + jq) * a.num_heads + h) *
-                                                          kHeadDim + 32 * c8);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) x[k] = src[k];
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  int pgv;
-  {
-    const int32_t* bt_row = a.block_table + (int64_t)it.req * a.bt_stride;
-    const uint32_t tok0 = (uint32_t)(split + nsplit * lane) * kStepTok + kTile * w;
-    const uint32_t pidx = fast_div(tok0, a.bs_div);
-    const bool ok = lane < nst && (int)tok0 < prefix && (int)pidx < a.bt_cols;
-    const int p = bt_row[ok ? pidx : 0];
-    pgv = ok ? p : -1;
-  }
-  auto tile_page = [&](int k) {
-    const int p = __builtin_amdgcn_readlane(pgv, k);
-    return (p >= 0 && p < a.num_pages) ? p : -1;
-  };
-  auto tile_pos = [&](int k) { return (split + nsplit * k) * kStepTok + kTile * w; };
-  auto issue = [&](int k) {
-    load_wide_tile(a, S.ring[w][k % kWdRing], tile_page(k), tile_pos(k), prefix, kvh, lane);
-  };
-
-  // ---- Q^T operand (permuted K dimension, fp16 high + low parts) and row sums ----
-  // Thread (r8, c8): features 32 c8 .. + 31 of row r8 are the four operand
-  // vectors (m = 2 (2 (c8 & 3) + jl) + aa, half c8 >> 2); slot 2i + b of
-  // vector (jl, aa) is local feature 16 jl + 4 aa + i + 8b.
-  {
-    float qs = 0.f;
-    const int gg = c8 >> 2;
-#pragma unroll
-    for (int jl = 0; jl < 2; ++jl) {
-#pragma unroll
-      for (int aa = 0; aa < 2; ++aa) {
-        half8 v, vl;
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int k = 16 * jl + 4 * aa + (u >> 1) + 8 * (u & 1);
-          const float xq = x[k >> 2][k & 3];
-          v[u] = (_Float16)xq;
-          vl[u] = (_Float16)(xq - (float)v[u]);
-          qs += xq;
-        }
-        const int m = 2 * (2 * (c8 & 3) + jl) + aa;
-        if (r8 < kWdRows) {
-          const bool ok = r8 < rows;
-          *reinterpret_cast<half8*>(&S.q[((m * 2 + gg) * kWdRows + r8) * 8]) = ok ? v : half8{};
-          *reinterpret_cast<half8*>(&S.qlo[((m * 2 + gg) * kWdRows + r8) * 8]) = ok ? vl : half8{};
-        }
-      }
-    }
-    qs += shfl_xor_f32(qs, 1);
-    qs += shfl_xor_f32(qs, 2);
-    qs += shfl_xor_f32(qs, 4);
-    if (c8 == 0 && r8 < kWdRows) S.qsum[r8] = r8 < rows ? qs : 0.f;
-  }
-  issue(0);
-  lds_barrier();
-  const float qsum = j < kWdRows ? S.qsum[j] : 0.f;
-  const bool qrow = j < kWdRows;
-  auto qop = [&](int m, bool lo) -> half8 {
-    const _Float16* base = lo ? S.qlo : S.q;
-    return qrow ? *reinterpret_cast<const half8*>(&base[((m * 2 + g) * kWdRows + j) * 8]) : half8{};
-  };
-
-  floatx16 acc[4][2];              // O^T blocks (q, b)
-#pragma unroll
-  for (int q = 0; q < 4; ++q) acc[q][0] = acc[q][1] = floatx16{};
-  float m_run = -__builtin_inff();
-  float l_run = 0.f, z_run = 0.f, ps_run = 0.f;     // this lane's share (its 16 tokens) of row j's sums
-  const uint32_t ones16 = magic_ones();
-  const uint32_t e2 = 2u * (uint32_t)(j & 1);
-  const uint32_t ls0 = 8u - e2, rs0 = e2, ls1 = 4u - e2, rs1 = 4u + e2;
-  SmallTileLds& T = S.tile[w];
-  constexpr int kSlotTok[8] = {0, 2, 1, 3, 4, 6, 5, 7};
-  // score register of token 16s + 8g + v (v < 8) in lane group g
-  auto reg_of = [](int s, int v) { return 8 * s + v; };
-
-  auto raise_max = [&](float mb, bool eager) {
-    mb = xor32_max(mb);
-    const bool need = mb > m_run + (eager ? 0.f : kLazy);
-    const bool resc = need && m_run != -__builtin_inff();
-    if (__ballot(resc)) {
-      const float alpha = resc ? exp2_raw(m_run - mb) : 1.f;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        acc[q][0] *= alpha;
-        acc[q][1] *= alpha;
-      }
-      l_run *= alpha;
-      z_run *= alpha;
-      ps_run *= alpha;
-    }
-    if (need) m_run = mb;
-    return m_run == -__builtin_inff() ? 0.f : m_run;
-  };
-
-  auto tile_body = [&](const SmallSlot& L, int k, int nvalid, uint32_t wm) {
-    // Tile k + 1 goes into the slot tile k - 1 left (its LDS reads are complete: lgkmcnt(0)).
-    if (k + 1 < nst) {
-      __builtin_amdgcn_s_waitcnt(0xC07F);
-      asm volatile("" ::: "memory");
-      issue(k + 1);
-    }
-    // ---- token parameters (lane t < 32) and the byte-transposed V codes ----
-    bool big;
-    {
-      const int t = lane & 31;
-      const bool used = t < nvalid && !((wm >> t) & 1u);
-      const u32x2 meta = L.meta[t];
-      const float ksc = f16_bits_to_f32(meta[0]);
-      const float kz = f16_bits_to_f32(meta[0] >> 16);
-      const float vsc = f16_bits_to_f32(meta[1]);
-      const float vz = f16_bits_to_f32(meta[1] >> 16);
-      if (lane < kTile) {
-        const float rvs = used ? 1.f / vsc : 0.f;
-        T.prm[0][t] = used ? 4.f * ksc * a.scale_log2 : 0.f;
-        T.prm[1][t] = used ? (kz - 4.f * ksc) * a.scale_log2 : 0.f;
-        T.prm[2][t] = used ? 0.f : -__builtin_inff();
-        T.prm[3][t] = used ? vsc : 0.f;
-        T.prm[4][t] = rvs;
-        T.prm[5][t] = used ? vz * rvs : 0.f;
-      }
-      big = __ballot(used && vsc > kLazyVsMax) != 0;
-      const int tq = lane & 7, bg = lane >> 3;
-      u32x2 vc[4];
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) vc[kk] = *reinterpret_cast<const u32x2*>(&L.vc[4 * tq + kk][8 * bg]);
-      uint32_t o0[4], o1[4];
-      transpose4(vc[0][0], vc[1][0], vc[2][0], vc[3][0], o0);
-      transpose4(vc[0][1], vc[1][1], vc[2][1], vc[3][1], o1);
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        T.vt[(8 * bg + kk) * kSmVtRow + tq] = o0[kk];
-        T.vt[(8 * bg + 4 + kk) * kSmVtRow + tq] = o1[kk];
-      }
-    }
-
-    // ---- S^T = K Q^T (both q parts) ----
-    floatx16 sc = floatx16{};
-    const u32x4 kc0 = L.kc[0][lane], kc1 = L.kc[1][lane];
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-      half8 ka[2];
-      k_operands(jj < 4 ? kc0[jj] : kc1[jj - 4], ones16, ka);
-#pragma unroll
-      for (int aa = 0; aa < 2; ++aa) {
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[aa], qop(2 * jj + aa, false), sc, 0, 0, 0);
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[aa], qop(2 * jj + aa, true), sc, 0, 0, 0);
-      }
-    }
-    wave_sync_lds();
-
-    // ---- scores of row j, tokens 16s + 8g + 4 hh + i (register 8s + 4hh + i) ----
-    float mb = -__builtin_inff();
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int t0 = 16 * s + 8 * g + 4 * hh;
-        const floatx4 av = *reinterpret_cast<const floatx4*>(&T.prm[0][t0]);
-        const floatx4 bv = *reinterpret_cast<const floatx4*>(&T.prm[1][t0]);
-        const floatx4 tmv = *reinterpret_cast<const floatx4*>(&T.prm[2][t0]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int rr = 8 * s + 4 * hh + i;
-          sc[rr] = fmaf(av[i], sc[rr], bv[i] * qsum) + tmv[i];
-          mb = fmaxf(mb, sc[rr]);
-        }
-      }
-    }
-    const float m_use = raise_max(mb, big);
-
-    // ---- P' = p * vs per k-step s, in the PV token order, and O^T += V^T P'^T ----
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      half8 pop;
-      {
-        const int t0 = 16 * s + 8 * g;
-        const floatx4 vs0 = *reinterpret_cast<const floatx4*>(&T.prm[3][t0]);
-        const floatx4 vs1 = *reinterpret_cast<const floatx4*>(&T.prm[3][t0 + 4]);
-        const floatx4 rv0 = *reinterpret_cast<const floatx4*>(&T.prm[4][t0]);
-        const floatx4 rv1 = *reinterpret_cast<const floatx4*>(&T.prm[4][t0 + 4]);
-        const floatx4 zv0 = *reinterpret_cast<const floatx4*>(&T.prm[5][t0]);
-        const floatx4 zv1 = *reinterpret_cast<const floatx4*>(&T.prm[5][t0 + 4]);
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int v = kSlotTok[u];
-          const float p = exp2_raw(sc[reg_of(s, v)] - m_use);
-          const float vs = v < 4 ? vs0[v] : vs1[v - 4];
-          const float rv = v < 4 ? rv0[v] : rv1[v - 4];
-          const float zv = v < 4 ? zv0[v] : zv1[v - 4];
-          const _Float16 hp = (_Float16)(p * vs);
-          pop[u] = hp;
-          const float wh = (float)hp;
-          ps_run += wh;
-          l_run = fmaf(wh, rv, l_run);
-          z_run = fmaf(wh, zv, z_run);
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const u32x2 d = *reinterpret_cast<const u32x2*>(&T.vt[(16 * q + (j >> 1)) * kSmVtRow + 4 * s + 2 * g]);
-        const half8 v0 = as_half8(pair_lo(d[0], ls0, ones16), pair_hi(d[0], rs0, ones16),
-                                  pair_lo(d[1], ls0, ones16), pair_hi(d[1], rs0, ones16));
-        const half8 v1 = as_half8(pair_lo(d[0], ls1, ones16), pair_hi(d[0], rs1, ones16),
-                                  pair_lo(d[1], ls1, ones16), pair_hi(d[1], rs1, ones16));
-        acc[q][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v0, pop, acc[q][0], 0, 0, 0);
-        acc[q][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v1, pop, acc[q][1], 0, 0, 0);
-      }
-    }
-  };
-
-  auto window_bits = [&](int k, int own) -> uint32_t {
-    if (!arena) return 0u;
-    const int page = tile_page(k);
-    const int pos = tile_pos(k) + (lane & 31);
-    const bool st = page >= 0 && pos < prefix && (pos < win_head || pos >= win_tail) && own == page;
-    return (uint32_t)__ballot(st);
-  };
-
-  uint64_t wtiles = 0;
-#pragma unroll 1
-  for (int k = 0; k < nst; ++k) {
-    // wait for tile k's loads (tile k + 1 is requested in the tile body)
-    wait_vmcnt<0>();
-    asm volatile("" ::: "memory");
-    const SmallSlot& L = S.ring[w][k % kWdRing];
-    const int page = tile_page(k);
-    const int nvalid = page >= 0 ? min(kTile, max(prefix - tile_pos(k), 0)) : 0;
-    const uint32_t wm = window_bits(k, (int)L.own[lane & 31][0]);
-    if (wm != 0u) {
-      wtiles |= 1ull << k;
-      S.wbits[w][k] = wm;
-    }
-    tile_body(L, k, nvalid, wm);
-  }
-
-  // ---- the window tokens: K from the fp16 image (high and low parts, half
-  // the k-steps at a time), V from the V image, p / 4 into the same accumulators ----
-#pragma unroll 1
-  while (wtiles != 0ull) {
-    const int k = __builtin_ctzll(wtiles);
-    wtiles &= wtiles - 1;
-    const int page = tile_page(k);
-    const int prow0 = (int)fast_mod((uint32_t)tile_pos(k), a.bs_div);
-    const uint32_t wm = __builtin_amdgcn_readfirstlane(S.wbits[w][k]);
-    const int64_t img = image_index(a, page, prow0, kvh);
-    const u32x4* kimg = reinterpret_cast<const u32x4*>(a.kimg + img * kKImgHalfs);
-    const int tl = swap23(j);                                   // this lane's token as an A row
-    const bool wl = (wm >> tl) & 1u;
-    floatx16 sc = floatx16{};
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      u32x4 khi[8], klo[8];
-#pragma unroll
-      for (int mm = 0; mm < 8; ++mm) {
-        const int m = 8 * half + mm;
-        khi[mm] = wl ? kimg[m * 64 + tl + 32 * g] : u32x4{};
-        klo[mm] = wl ? kimg[kImgHalfs / 8 + m * 64 + tl + 32 * g] : u32x4{};
-      }
-#pragma unroll
-      for (int mm = 0; mm < 8; ++mm) {
-        const int m = 8 * half + mm;
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, khi[mm]), qop(m, false), sc, 0, 0, 0);
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, khi[mm]), qop(m, true), sc, 0, 0, 0);
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, klo[mm]), qop(m, false), sc, 0, 0, 0);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    const half8* vimg = reinterpret_cast<const half8*>(a.vimg + img * kImgHalfs);
-    half8 vv[4][2][2];             // block (q, b), k-step s
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int s = 0; s < 2; ++s) vv[q][b][s] = vimg[((q * 2 + b) * 2 + s) * 64 + lane];
-    float mb = -__builtin_inff();
-#pragma unroll
-    for (int rr = 0; rr < 16; ++rr) {
-      const int tok = 16 * (rr >> 3) + 8 * g + (rr & 7);
-      sc[rr] = ((wm >> tok) & 1u) ? sc[rr] * a.scale_log2 : -__builtin_inff();
-      mb = fmaxf(mb, sc[rr]);
-    }
-    const float m_use = raise_max(mb, false);
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      half8 pwop;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const _Float16 hw = (_Float16)(0.25f * exp2_raw(sc[reg_of(s, kSlotTok[u])] - m_use));
-        pwop[u] = hw;
-        l_run = fmaf(4.f, (float)hw, l_run);
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-          acc[q][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vv[q][b][s], pwop, acc[q][b], 0, 0, 0);
-    }
-  }
-
-  // ---- the four wavefronts' rows combined into the split's partial:
-  // (w0 + w2) + (w1 + w3), each scaled to the common maximum ----
-  l_run = xor32_sum(l_run);
-  z_run = xor32_sum(z_run);
-  ps_run = xor32_sum(ps_run);
-  lds_barrier();                                   // every wavefront is past its last tile
-  WideCombineLds& C = *reinterpret_cast<WideCombineLds*>(smem_raw);
-  if (lane < kRows) C.m[w][lane] = m_run;
-  lds_barrier();
-  float M = C.m[0][j];
-#pragma unroll
-  for (int ww = 1; ww < kWaves; ++ww) M = fmaxf(M, C.m[ww][j]);
-  const float alpha = m_run == -__builtin_inff() ? 0.f : exp2_raw(m_run - M);
-  // sum_t p (c vs + vz) = 4 * acc - 4 * sum_t P' + sum_t p vz, scaled to the common maximum
-  const float off = alpha * (z_run - 4.f * ps_run);
-  const float a4 = 4.f * alpha;
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[q][b][i] = fmaf(a4, acc[q][b][i], off);
-  if (g == 0) C.l[w][j] = alpha * l_run;
-  // registers 4jq + 2h + e of blocks (q, b): features 64q + 16jq + 8g + 4h + 2b + e of row j
-  auto put = [&](int buf) {
-    if (j < kWdRows) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int jq = 0; jq < 4; ++jq)
-#pragma unroll
-          for (int h = 0; h < 2; ++h)
-            *reinterpret_cast<floatx4*>(&C.o[buf][j][64 * q + 16 * jq + 8 * g + 4 * h]) =
-                floatx4{acc[q][0][4 * jq + 2 * h], acc[q][0][4 * jq + 2 * h + 1], acc[q][1][4 * jq + 2 * h],
-                        acc[q][1][4 * jq + 2 * h + 1]};
-    }
-  };
-  auto add = [&](int buf) {
-    if (j < kWdRows) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int jq = 0; jq < 4; ++jq)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const floatx4 o = *reinterpret_cast<const floatx4*>(&C.o[buf][j][64 * q + 16 * jq + 8 * g + 4 * h]);
-            acc[q][0][4 * jq + 2 * h] += o[0];
-            acc[q][0][4 * jq + 2 * h + 1] += o[1];
-            acc[q][1][4 * jq + 2 * h] += o[2];
-            acc[q][1][4 * jq + 2 * h + 1] += o[3];
-          }
-    }
-  };
-  lds_barrier();                                   // the maxima are read
-  if (w >= 2) put(w - 2);
-  lds_barrier();
-  if (w < 2) add(w);
-  lds_barrier();
-  if (w == 1) put(0);
-  lds_barrier();
-  const int nrow = min(kWdRows, rows);
-  float* part = a.ws + partial_index(a, it, split, 0) * kPartialFloats;
-  if (w == 0) {
-    add(0);
-    if (j < nrow) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int jq = 0; jq < 4; ++jq)
-#pragma unroll
-          for (int h = 0; h < 2; ++h)
-            *reinterpret_cast<floatx4*>(part + j * kHeadDim + 64 * q + 16 * jq + 8 * g + 4 * h) =
-                floatx4{acc[q][0][4 * jq + 2 * h], acc[q][0][4 * jq + 2 * h + 1], acc[q][1][4 * jq + 2 * h],
-                        acc[q][1][4 * jq + 2 * h + 1]};
-    }
-    if (lane < nrow) {
-      part[kPartO + lane] = M;
-      part[kPartO + kRows + lane] = (C.l[0][lane] + C.l[1][lane]) + (C.l[2][lane] + C.l[3][lane]);
-    }
-  }
-  if (fresh_here) {
-    __syncthreads();
-    const int ftid = 64 * w + (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
-    fresh_partial(a, it, item, 0, *reinterpret_cast<FreshLds*>(smem_raw), ftid);
-  }
-}
-
 // One 256-thread block per (output row, quarter of the features) of an item.
 // Every load the block needs goes out in one round: the partials' (m, l)
 // (thread per partial) and the block's 64-feature slice of every partial row
@@ -2610,15 +1971,14 @@ int fill_common(DecodeArgs& a, const float* q_rot, int32_t num_heads, int32_t nu
   return kOk;
 }
 
-std::atomic<uint64_t> g_split_lds_set[4] = {{0}, {0}, {0}, {0}};
+std::atomic<uint64_t> g_split_lds_set[3] = {{0}, {0}, {0}};
 
 int set_split_lds() {
-  const void* k[4] = {reinterpret_cast<const void*>(paged_decode_split_kernel<false, false>),
-                      reinterpret_cast<const void*>(paged_decode_split_kernel<true, false>),
-                      reinterpret_cast<const void*>(paged_decode_split_small_kernel),
-                      reinterpret_cast<const void*>(paged_decode_split_wide_kernel)};
-  const size_t bytes[4] = {kLdsBytes, kLdsBytes, kSmallLdsBytes, kWideLdsBytes};
-  for (int i = 0; i < 4; ++i) {
+  const void* k[3] = {reinterpret_cast<const void*>(paged_decode_split_kernel<false>),
+                      reinterpret_cast<const void*>(paged_decode_split_kernel<true>),
+                      reinterpret_cast<const void*>(paged_decode_split_small_kernel)};
+  const size_t bytes[3] = {kLdsBytes, kLdsBytes, kSmallLdsBytes};
+  for (int i = 0; i < 3; ++i) {
     const int rc = set_dynamic_lds(k[i], (int)bytes[i], g_split_lds_set[i]);
     if (rc != kOk) return rc;
   }
@@ -2633,9 +1993,9 @@ unsigned split_workgroups(const DecodeArgs& a) {
   return (unsigned)n;
 }
 
-// Split kernel instance of a launch chunk: the mid-step load issue when some
-// item has more 128-token steps than there are splits, with the small-row
-// score tile when no item has more than 8 rows.
+// Split kernel of a launch chunk: the small-row kernel when no item has more
+// than 8 rows; else the cooperative kernel, with the mid-step load issue when
+// some item has more 128-token steps than it has splits.
 void launch_split(const DecodeArgs& a, unsigned nitems, dim3 grid, hipStream_t stream) {
   bool multi = false;
   int64_t max_rows = 0;
@@ -2648,12 +2008,10 @@ void launch_split(const DecodeArgs& a, unsigned nitems, dim3 grid, hipStream_t s
   }
   if (max_rows <= kSmRows)
     hipLaunchKernelGGL(paged_decode_split_small_kernel, grid, dim3(256), kSmallLdsBytes, stream, a);
-  else if (multi && max_rows <= kWdRows)
-    hipLaunchKernelGGL(paged_decode_split_wide_kernel, grid, dim3(256), kWideLdsBytes, stream, a);
   else if (multi)
-    hipLaunchKernelGGL((paged_decode_split_kernel<true, false>), grid, dim3(256), kLdsBytes, stream, a);
+    hipLaunchKernelGGL((paged_decode_split_kernel<true>), grid, dim3(256), kLdsBytes, stream, a);
   else
-    hipLaunchKernelGGL((paged_decode_split_kernel<false, false>), grid, dim3(256), kLdsBytes, stream, a);
+    hipLaunchKernelGGL((paged_decode_split_kernel<false>), grid, dim3(256), kLdsBytes, stream, a);
 }
 
 // Merge blocks per feature quarter: one per row of a row tile that can hold
