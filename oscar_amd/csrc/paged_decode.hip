@@ -722,22 +722,26 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
         }
       }
     }
-    // The window tiles' V image blocks of this wave's features are requested
-    // here, a phase before the PV pass uses them.
+    // The window tiles' V image blocks of this wave's features (high parts)
+    // are requested here, a phase before the PV pass uses them.  The low
+    // parts share their cache lines and replace them in the PV pass.
     const bool anywin = (wm0 | wm1 | wm2 | wm3) != 0u;
+    auto vimg_of = [&](int j) {
+      return reinterpret_cast<const half8*>(
+          a.vimg + image_index(a, pgs[j], (int)fast_mod((uint32_t)(tbase + kTile * j), a.bs_div), kvh) *
+                       kVImgHalfs);
+    };
     half8 vim[kWaves][2][2];
     if (anywin) {
 #pragma unroll
       for (int j = 0; j < kWaves; ++j) {
         const uint32_t wmj = j == 0 ? wm0 : (j == 1 ? wm1 : (j == 2 ? wm2 : wm3));
         if (wmj != 0u) {
-          const half8* vimg = reinterpret_cast<const half8*>(
-              a.vimg + image_index(a, pgs[j], (int)fast_mod((uint32_t)(tbase + kTile * j), a.bs_div), kvh) *
-                           kImgHalfs);
+          const half8* vimg = vimg_of(j);
 #pragma unroll
           for (int b = 0; b < 2; ++b)
 #pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2) vim[j][b][s2] = vimg[((w * 2 + b) * 2 + s2) * 64 + lane];
+            for (int s2 = 0; s2 < 2; ++s2) vim[j][b][s2] = vimg[vimg_part(((w * 2 + b) * 2 + s2) * 64 + lane, 0)];
         }
       }
     }
@@ -849,6 +853,29 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
 #pragma unroll
           for (int b = 0; b < 2; ++b)
             acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vim[j][b][s2], pwop, acc[b], 0, 0, 0);
+        }
+        // the low parts into the same registers (cache lines the high parts
+        // brought in), multiplied in after the last tile
+        const half8* vimg = vimg_of(j);
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) vim[j][b][s2] = vimg[vimg_part(((w * 2 + b) * 2 + s2) * 64 + lane, 1)];
+      }
+    }
+    if (anywin) {
+#pragma unroll
+      for (int j = 0; j < kWaves; ++j) {
+        const uint32_t wmj = j == 0 ? wm0 : (j == 1 ? wm1 : (j == 2 ? wm2 : wm3));
+        if (wmj != 0u) {
+          const _Float16* pwr = &S.pw[j][col * kPRow + 8 * g];
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) {
+            const half8 pwop = *reinterpret_cast<const half8*>(pwr + 16 * s2);
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+              acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vim[j][b][s2], pwop, acc[b], 0, 0, 0);
+          }
         }
       }
     }
@@ -1371,15 +1398,18 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(Decode
       for (int h = 0; h < 2; ++h)
         sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, khi[h][s]), qa, sc[h], 0, 0, 0);
     }
-    // the V image (feature tile n = 4q + 2mh + b: chunk (q, b, G >> 1), lane
-    // 16 mh + c + 32 (G & 1)) requested as soon as the high parts are used,
-    // into their registers (kept below the high-part MFMAs)
+    // the V image's high part (feature tile n = 4q + 2mh + b: chunk (q, b,
+    // G >> 1), lane 16 mh + c + 32 (G & 1)) requested as soon as K's high
+    // parts are used, into their registers, and its low part likewise after
+    // K's low parts (the barriers keep the loads below those MFMAs)
     __builtin_amdgcn_sched_barrier(0);
-    const half8* vimg = reinterpret_cast<const half8*>(a.vimg + img * kImgHalfs);
-    half8 vv[16];
+    const half8* vimg = reinterpret_cast<const half8*>(a.vimg + img * kVImgHalfs);
+    auto vimg_index = [&](int n) {
+      return (((n >> 2) * 2 + (n & 1)) * 2 + (G >> 1)) * 64 + 16 * ((n >> 1) & 1) + c + 32 * (G & 1);
+    };
+    half8 vv[16], vl[16];
 #pragma unroll
-    for (int n = 0; n < 16; ++n)
-      vv[n] = vimg[(((n >> 2) * 2 + (n & 1)) * 2 + (G >> 1)) * 64 + 16 * ((n >> 1) & 1) + c + 32 * (G & 1)];
+    for (int n = 0; n < 16; ++n) vv[n] = vimg[vimg_part(vimg_index(n), 0)];
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       const half8 qa = S.qt[s][lane];
@@ -1387,6 +1417,9 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(Decode
       for (int h = 0; h < 2; ++h)
         sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, klo[h][s]), qa, sc[h], 0, 0, 0);
     }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int n = 0; n < 16; ++n) vl[n] = vimg[vimg_part(vimg_index(n), 1)];
     float sv[8];
     float mb = -__builtin_inff();
     const uint32_t wb = wm >> (8 * G);
@@ -1408,6 +1441,8 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(Decode
     }
 #pragma unroll
     for (int n = 0; n < 16; ++n) acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv[n], pwop, acc[n], 0, 0, 0);
+#pragma unroll
+    for (int n = 0; n < 16; ++n) acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl[n], pwop, acc[n], 0, 0, 0);
   }
 
   // ---- the four wavefronts' rows combined into the split's partial ----

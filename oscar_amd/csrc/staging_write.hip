@@ -39,7 +39,7 @@ struct StageArgs {
   int64_t* owner;           // [rows][bs]
   int32_t* winner;          // [rows][bs], -1 between calls
   _Float16* kimg;           // [rows][bs / 32][Hk][kKImgHalfs] or null
-  _Float16* vimg;           // [rows][bs / 32][Hk][kImgHalfs] or null
+  _Float16* vimg;           // [rows][bs / 32][Hk][kVImgHalfs] or null
 };
 
 __device__ __forceinline__ int64_t seat_of(int64_t slot, const StageArgs& a) {
@@ -102,8 +102,9 @@ __global__ __launch_bounds__(256) void stage_update_kernel(StageArgs a) {
       const int prow = (int)(seat % a.block_size);
       const int64_t img = ((seat / a.block_size) * (a.block_size / 32) + prow / 32) * a.num_kv_heads + h;
       _Float16* kd = a.kimg + img * kKImgHalfs + kimg_offset(f, prow & 31);
-      k_parts(yk, kd[0], kd[kImgHalfs]);
-      a.vimg[img * kImgHalfs + vimg_offset(f, prow & 31)] = (_Float16)yv;
+      fp16_parts(yk, kd[0], kd[kImgHalfs]);
+      _Float16* vd = a.vimg + img * kVImgHalfs + vimg_offset(f, prow & 31);
+      fp16_parts(yv, vd[0], vd[kVPartHalfs]);
     }
   }
 }

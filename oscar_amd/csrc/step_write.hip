@@ -273,17 +273,13 @@ __device__ void write_vector(const WriteCtx& a, const floatx4& y, int t, int h, 
   if (a.img != nullptr) {
     const int64_t tile = image_of(arow, (int)prow, a.block_size, h, a.num_kv_heads);
     const int tt = (int)(prow & 31);
-    if (side == 0) {
-      _Float16* img = a.img + tile * kKImgHalfs;
+    static_assert(kKImgHalfs == kVImgHalfs, "one image stride for both sides");
+    _Float16* img = a.img + tile * kKImgHalfs;
+    const int lo = side == 0 ? kImgHalfs : kVPartHalfs;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        _Float16* d = img + kimg_offset(4 * lane + c, tt);
-        k_parts(y[c], d[0], d[kImgHalfs]);
-      }
-    } else {
-      _Float16* img = a.img + tile * kImgHalfs;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) img[vimg_offset(4 * lane + c, tt)] = (_Float16)y[c];
+    for (int c = 0; c < 4; ++c) {
+      _Float16* d = img + (side == 0 ? kimg_offset(4 * lane + c, tt) : vimg_offset(4 * lane + c, tt));
+      fp16_parts(y[c], d[0], d[lo]);
     }
   }
 }

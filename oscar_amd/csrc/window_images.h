@@ -2,11 +2,13 @@
 // kernels, read by the paged decode), per (arena row, 32-token tile, kv head):
 //   K image [2 parts][16 k-steps m][64 lanes][8 slots]: lane t + 32g, slot
 //     2i + b of step m = 2j + a holds feature 128g + 16j + 4a + i + 8b of
-//     token t; part 0 is RNE fp16(k), part 1 RNE fp16(k - part 0), so that
-//     the two parts carry k to about 2^-22 of its magnitude;
-//   V image [4 q][2 b][2 s][64 lanes][8 slots]: lane m + 32gs holds feature
-//     64q + 4(m >> 1) + 2b + (m & 1); slot u holds token 16s + 8gs +
-//     {0, 2, 1, 3, 4, 6, 5, 7}[u].
+//     token t;
+//   V image [4 q][2 b][2 s][64 lanes][2 parts][8 slots]: lane m + 32gs holds
+//     feature 64q + 4(m >> 1) + 2b + (m & 1); slot u holds token 16s + 8gs +
+//     {0, 2, 1, 3, 4, 6, 5, 7}[u] (a lane's two parts are adjacent, so that
+//     loading the high parts brings the low parts' cache lines too).
+// In both, part 0 is RNE fp16(x) and part 1 RNE fp16(x - part 0), so that the
+// two parts carry the FP32 value to about 2^-22 of its magnitude.
 // Both are exactly MFMA operand registers of the decode's wavefronts (K: the
 // tile's owner, V: wavefront q's quarter of the features), which read them
 // with one 16-byte load per lane and block.
@@ -16,11 +18,12 @@
 
 namespace oscar {
 
-constexpr int kImgHalfs = 16 * 64 * 8;     // one operand image (V image; one K part)
+constexpr int kImgHalfs = 16 * 64 * 8;     // one part of an operand image
 constexpr int kKImgHalfs = 2 * kImgHalfs;  // K image: high part, then low part
+constexpr int kVImgHalfs = 2 * kImgHalfs;  // V image: high and low part of each lane's 8 slots
 
-// The two fp16 parts of a K value.
-__device__ __forceinline__ void k_parts(float x, _Float16& hi, _Float16& lo) {
+// The two fp16 parts of a window value.
+__device__ __forceinline__ void fp16_parts(float x, _Float16& hi, _Float16& lo) {
   hi = (_Float16)x;
   lo = (_Float16)(x - (float)hi);
 }
@@ -32,12 +35,18 @@ __device__ __forceinline__ int kimg_offset(int f, int t) {
   return (m * 64 + t + 32 * g) * 8 + u;
 }
 
+// (V: the high part; the low part follows 8 halves later.)
 __device__ __forceinline__ int vimg_offset(int f, int t) {
   const int q = f >> 6, b = (f >> 1) & 1, m = 2 * ((f >> 2) & 15) + (f & 1);
   const int s = t >> 4, gs = (t >> 3) & 1, r = t & 7;
   const int slot = r == 1 ? 2 : (r == 2 ? 1 : (r == 5 ? 6 : (r == 6 ? 5 : r)));   // self-inverse
-  return ((((q * 2 + b) * 2 + s) * 64) + m + 32 * gs) * 8 + slot;
+  return ((((q * 2 + b) * 2 + s) * 64) + m + 32 * gs) * 16 + slot;
 }
+constexpr int kVPartHalfs = 8;             // low part of a V slot: 8 halves after the high part
+
+// Index, in 8-half vectors, of part `part` of lane-block `lb` (block * 64 +
+// lane) of a V image.
+__device__ __forceinline__ int vimg_part(int lb, int part) { return 2 * lb + part; }
 
 // Image of the 32-token tile holding arena seat row `prow` of arena row
 // `arow`, kv head h.

@@ -40,8 +40,9 @@ def _v_image_tokens() -> torch.Tensor:
 
 
 def image_shape(rows: int, bs: int, hk: int) -> tuple:
-    """Shape of the V operand image of an arena."""
-    return (rows, bs // 32, hk, IMAGE_HALFS)
+    """Shape of the V operand image of an arena: a high and a low fp16 part
+    per lane slot."""
+    return (rows, bs // 32, hk, 2 * IMAGE_HALFS)
 
 
 def k_image_shape(rows: int, bs: int, hk: int) -> tuple:
@@ -78,10 +79,10 @@ def check_images(k_image, v_image, rows: int, bs: int, hk: int) -> None:
 
 def stage_images(stage_k: torch.Tensor, stage_v: torch.Tensor):
     """fp16 operand images of a whole arena (the layout oscar_staging_write
-    maintains incrementally): K [rows][bs/32][Hk][part][m][lane = t + 32g][slot]
-    with part 0 = RNE fp16(k) and part 1 = RNE fp16(k - part 0),
-    V [rows][bs/32][Hk][q][b][s][lane = m + 32gs][slot] with feature
-    64q + 4(m // 2) + 2b + m % 2."""
+    maintains incrementally): K [rows][bs/32][Hk][part][m][lane = t + 32g][slot],
+    V [rows][bs/32][Hk][q][b][s][lane = m + 32gs][part][slot] with feature
+    64q + 4(m // 2) + 2b + m % 2; part 0 = RNE fp16(x), part 1 = RNE
+    fp16(x - part 0)."""
     rows, bs, hk, d = stage_k.shape
     if d != 256 or bs % 32:
         raise ValueError("operand images need D = 256 and a block size that is a multiple of 32")
@@ -95,11 +96,13 @@ def stage_images(stage_k: torch.Tensor, stage_v: torch.Tensor):
         x = x.view(rows, T, 32, hk, 2, 16, 8).permute(0, 1, 3, 5, 4, 2, 6)  # [r, T, hk, m, g, t, u]
         parts.append(x.reshape(rows, T, hk, IMAGE_HALFS))
     kimg = torch.cat(parts, -1).contiguous()
-    y = stage_v.view(rows, T, 32, hk, d).to(torch.float16).permute(0, 1, 3, 4, 2)  # [r, T, hk, f, tok]
-    y = y[..., _v_image_tokens().to(dev)]                                    # [r, T, hk, f, (s, gs, u)]
-    y = y.reshape(rows, T, hk, 4, 16, 2, 2, 2, 2, 8)                        # f = (q, bl, b, e)
-    y = y.permute(0, 1, 2, 3, 5, 7, 8, 4, 6, 9)                              # [r, T, hk, q, b, s, gs, (bl, e), u]
-    vimg = y.reshape(rows, T, hk, IMAGE_HALFS).contiguous()
+    yf = stage_v.view(rows, T, 32, hk, d).float().permute(0, 1, 3, 4, 2)   # [r, T, hk, f, tok]
+    yf = yf[..., _v_image_tokens().to(dev)].reshape(rows, T, hk, d, 2, 2, 8)  # [r, T, hk, f, s, gs, u]
+    yh = yf.to(torch.float16)
+    y = torch.stack((yh, (yf - yh.float()).to(torch.float16)), -2)          # [r, T, hk, f, s, gs, part, u]
+    y = y.reshape(rows, T, hk, 4, 16, 2, 2, 2, 2, 2, 8)                     # f = (q, bl, b, e)
+    y = y.permute(0, 1, 2, 3, 5, 7, 8, 4, 6, 9, 10)                          # [r, T, hk, q, b, s, gs, (bl, e), part, u]
+    vimg = y.reshape(rows, T, hk, 2 * IMAGE_HALFS).contiguous()
     return kimg, vimg
 
 

@@ -3,7 +3,8 @@
 Each case draws page size, kv heads / group, request count, history and
 query lengths (page edges included), window geometry, and cache dtype.  It
 runs the MTP decode (1e-3 of the output scale), the DecodeOnly read over
-the same caches (1e-3), the pre-rotated quantize-write (bit-exact, random
+the same caches (1e-3; half that over a 1000-case sweep and on the
+window-heavy cases), the pre-rotated quantize-write (bit-exact, random
 caches, skipped and out-of-range slots, clip ratios), and the prefill
 continuation (bf16 contract 2e-2 + 2^-8 |oracle|).  The seeds are fixed, so
 the cases are the same on every run."""
@@ -40,8 +41,10 @@ def decode_cases(seed, n):
                    recent=recent, staging=staging, window=window, cache_dtype=cd)
 
 
-@pytest.mark.parametrize("params", list(decode_cases(7, 40)), ids=lambda p: f"seed{p['seed']}")
-def test_decode_routes_random_shapes(device, params):
+def route_errors(device, params):
+    """max |gpu - oracle| / max |oracle| of the MTP read and of the DecodeOnly
+    read of one random case (outputs checked finite)."""
+    params = dict(params)
     hist, qlens = params.pop("history"), params.pop("q_lens")
     case = decode_case(hist, qlens, **params)
     L = case.layer
@@ -53,13 +56,51 @@ def test_decode_routes_random_shapes(device, params):
     got = decode.paged_attention(q.to(device), k.to(device), v.to(device), kc, vc, bt, case.qsl, case.seqs,
                                  L.scale, dstage).cpu()
     assert torch.isfinite(got).all()
-    assert (got - want).abs().max() <= 1e-3 * max(want.abs().max().item(), 1e-6)
+    em = ((got - want).abs().max() / max(want.abs().max().item(), 1e-6)).item()
     last = q[[case.qsl[i + 1] - 1 for i in range(len(hist))]]
     arena = None if stage is None else (L.arena.stage_k, L.arena.stage_v, L.arena.owner, L.arena.sink_eff, L.recent)
     want = oatt.decode_only_ref(last, L.k_cache, L.v_cache, case.bt, case.seqs, L.scale, L.num_kv_heads, D, arena)
     got = decode.decode_only(last.to(device), kc, vc, bt, case.seqs, L.scale, dstage, L.sink, L.recent).cpu()
     assert torch.isfinite(got).all()
-    assert (got - want).abs().max() <= 1e-3 * max(want.abs().max().item(), 1e-6)
+    ed = ((got - want).abs().max() / max(want.abs().max().item(), 1e-6)).item()
+    return em, ed
+
+
+def check_both_routes(device, params, bar):
+    em, ed = route_errors(device, params)
+    assert em <= bar and ed <= bar, (em, ed)
+
+
+@pytest.mark.parametrize("params", list(decode_cases(7, 40)), ids=lambda p: f"seed{p['seed']}")
+def test_decode_routes_random_shapes(device, params):
+    check_both_routes(device, params, 1e-3)
+
+
+# Short requests the FP32 window holds almost entirely, where the staged
+# values dominate the output: the cases of the seeded sweeps above whose
+# error is largest when a staged V value enters the PV pass as a single fp16
+# part (5.0e-4 to 5.4e-4 of the output scale from that rounding alone, on the
+# oracle).  With the V image's high and low parts they keep half the bar.
+WINDOW_HEAVY = [(1234, 217), (7, 225), (7, 231), (7, 241)]
+
+
+@pytest.mark.parametrize("seed,index", WINDOW_HEAVY, ids=lambda x: str(x))
+def test_window_heavy_reads_keep_half_the_bar(device, seed, index):
+    params = list(decode_cases(seed, index + 1))[index]
+    assert params["window"]
+    check_both_routes(device, params, 5e-4)
+
+
+def test_decode_routes_sweep_1000(device):
+    """1000 seeded random cases through both read routes: the worst error of
+    each route stays within half the bar (measured worst: 3.6e-4 MTP, 2.6e-4
+    DecodeOnly)."""
+    worst_m = worst_d = 0.0
+    for params in decode_cases(1234, 1000):
+        em, ed = route_errors(device, params)
+        worst_m, worst_d = max(worst_m, em), max(worst_d, ed)
+    print(f"sweep worst: MTP {worst_m:.3e} DecodeOnly {worst_d:.3e}")
+    assert worst_m <= 5e-4 and worst_d <= 5e-4, (worst_m, worst_d)
 
 
 def write_prefill_cases(seed, n):

@@ -322,10 +322,11 @@ def test_plan_capacity_fits_one_mi355x():
 def test_operand_image_layouts_follow_their_formulas():
     """The fp16 window images the decode reads as MFMA operands, element by element:
     K block m, lane t + 32g, slot u = feature 128g + 16(m // 2) + 4(m % 2) + u // 2 + 8(u % 2)
-    of token t; V block (q, b, s), lane m + 32gs, slot u = feature 64q + 4(m // 2) + 2b + m % 2
-    of token 16s + 8gs + (0, 2, 1, 3, 4, 6, 5, 7)[u].  The K image's second part holds
-    fp16(k - fp16(k)) in the same order, so that the two parts sum to k within 2^-22 |k| + 2^-25
-    (half the spacing of fp16 subnormals, where the low part of a small k lies)."""
+    of token t; V block (q, b, s), lane m + 32gs, part p, slot u = feature 64q + 4(m // 2) + 2b + m % 2
+    of token 16s + 8gs + (0, 2, 1, 3, 4, 6, 5, 7)[u].  Each image's second part holds
+    fp16(x - fp16(x)) (K: a second image in the same order; V: the 8 halves after the lane's
+    high part), so that the two parts sum to x within 2^-22 |x| + 2^-25 (half the spacing of
+    fp16 subnormals, where the low part of a small x lies)."""
     from oscar_amd.kernels import staging as kstaging
 
     g = torch.Generator().manual_seed(3)
@@ -335,7 +336,7 @@ def test_operand_image_layouts_follow_their_formulas():
     order = [0, 2, 1, 3, 4, 6, 5, 7]
     for r, tile in ((0, 0), (1, 1)):
         K, KL = kimg[r, tile, 0].view(2, 16, 64, 8)
-        V = vimg[r, tile, 0].view(4, 2, 2, 64, 8)
+        V = vimg[r, tile, 0].view(4, 2, 2, 64, 2, 8)
         for lane in range(64):
             t, gg = lane % 32, lane // 32
             for m in range(16):
@@ -352,7 +353,10 @@ def test_operand_image_layouts_follow_their_formulas():
                         for u in range(8):
                             f = 64 * q + 4 * (mm // 2) + 2 * b + mm % 2
                             tok = 16 * s + 8 * gs + order[u]
-                            assert V[q, b, s, lane, u] == sv[r, 32 * tile + tok, 0, f].half()
+                            x = sv[r, 32 * tile + tok, 0, f]
+                            hi, lo = V[q, b, s, lane, 0, u], V[q, b, s, lane, 1, u]
+                            assert hi == x.half() and lo == (x - x.half().float()).half()
+                            assert abs(hi.double() + lo.double() - x.double()) <= 2.0 ** -22 * abs(x) + 2.0 ** -25
 
 
 def test_request_layout_is_built_once_per_step():
