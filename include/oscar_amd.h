@@ -100,9 +100,9 @@ int oscar_quant_write_prerotated(const float* k_rot, const float* v_rot, int64_t
  *     history positions 0 .. seq_lens[i] - n_i - 1;
  *   max_query_len / max_history: host upper bounds used to size the grid;
  *   stage_owner [stage_rows][block_size] int64 and the window's fp16 operand
- *     images stage_k_image [stage_rows][block_size / 32][Hk][16384] /
- *     stage_v_image [stage_rows][block_size / 32][Hk][8192] (16-byte
- *     aligned, written by oscar_staging_write; stage_rows = 0: no window);
+ *     images stage_k_image / stage_v_image, each
+ *     [stage_rows][block_size / 32][Hk][16384] (16-byte aligned, written by
+ *     the window writes; stage_rows = 0: no window);
  *   tiles_per_split: 32-token tiles per split workgroup (0: automatic, at most 256);
  *   out [num_tokens][Hq][D] fp32 (rotated-V domain);
  *   workspace: >= oscar_paged_decode_workspace_bytes(...) bytes (same
@@ -343,12 +343,14 @@ int oscar_mtp_forward(const oscar_mtp_layer* layer, const oscar_mtp_step* step, 
  * stage_rows, slot % block_size) the highest token index wins: owner = page
  * (kept) or -1, and a kept winner stores key @ rot_k / value @ rot_v (fp32,
  * unclipped).  key/value: bf16 [num_tokens][token_stride]; rot_*: fp32 [D][D];
- * seat_winner: int32 [stage_rows][block_size] scratch that must hold -1 on
- * entry and is left at -1.  stage_k_image / stage_v_image (both or neither,
- * block_size % 32 == 0): fp16 [stage_rows][block_size / 32][Hk][16384] (K:
- * the fp16 rounding of each value, then the fp16 rounding of what it left)
- * and [stage_rows][block_size / 32][Hk][8192] (V); a kept winner also
- * writes its values there in the decode kernel's MFMA operand order.
+ * seat_winner: int64 [stage_rows * block_size + 2], zero when allocated and
+ * kept by the caller across calls (never reset: a call tags its keys with an
+ * epoch it advances in the buffer's last two words).  stage_k_image /
+ * stage_v_image (both or neither, block_size % 32 == 0): fp16
+ * [stage_rows][block_size / 32][Hk][16384] each (the fp16 rounding of each
+ * value and the fp16 rounding of what it left: K as two 8192-half images, V
+ * as the two parts of each lane's 8 slots); a kept winner also writes its
+ * values there in the decode kernel's MFMA operand order.
  */
 int oscar_staging_write(const void* key_bf16, const void* value_bf16, int64_t token_stride,
                         const int64_t* slot_mapping, int32_t num_tokens,
@@ -356,8 +358,33 @@ int oscar_staging_write(const void* key_bf16, const void* value_bf16, int64_t to
                         int32_t num_requests, int32_t num_kv_heads, int32_t head_size,
                         int32_t block_size, int32_t stage_rows, int32_t sink_eff, int32_t recent,
                         const float* rot_k, const float* rot_v, float* stage_k, float* stage_v,
-                        int64_t* stage_owner, int32_t* seat_winner, void* stage_k_image,
+                        int64_t* stage_owner, int64_t* seat_winner, void* stage_k_image,
                         void* stage_v_image, oscar_stream_t stream);
+
+/* A prefill-sized step's whole write: oscar_quant_write and the window write
+ * of oscar_staging_write from the same rotated values, in two launches (a
+ * seat-winner pass over the step's slots, then the fused quantize-write
+ * kernel, whose epilogue writes the owner tags, the staged values and their
+ * images).  Replaces do_kv_cache_update followed by _staging_write
+ * (oscar_ascend/backend.py:150-189, 439-481).  Arguments: those of
+ * oscar_quant_write, then the step's request layout and the arena as for
+ * oscar_staging_write (stage_rows > 0).  The staged values are the fused
+ * kernel's MFMA rotation (the bf16 high + low split of R), which differs from
+ * an fp32 x @ R by about 2^-17 of the values' scale.  Writes of at most 2048
+ * vectors take oscar_step_write's kernel, window write included, in one
+ * launch.
+ */
+int oscar_quant_write_window(const void* key_bf16, const void* value_bf16, int64_t num_tokens,
+                             int32_t num_kv_heads, int32_t head_size, int64_t token_stride,
+                             const void* rot_k_operand, const void* rot_v_operand,
+                             const int64_t* slot_mapping, void* k_cache, void* v_cache,
+                             int32_t block_size, int64_t num_pages, int64_t k_stride_page,
+                             int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
+                             int64_t v_stride_token, int64_t v_stride_head, int32_t clip_index_k,
+                             int32_t clip_index_v, const int32_t* query_start_loc, const int32_t* seq_lens,
+                             int32_t num_requests, int32_t stage_rows, int32_t sink_eff, int32_t recent,
+                             float* stage_k, float* stage_v, int64_t* stage_owner, int64_t* seat_winner,
+                             void* stage_k_image, void* stage_v_image, oscar_stream_t stream);
 
 #ifdef __cplusplus
 }

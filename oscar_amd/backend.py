@@ -6,10 +6,13 @@ to a subclass of (this class, the native impl class) and calls
 ``_oscar_setup()``; vLLM then calls ``forward`` / ``do_kv_cache_update``.
 
 Write path (every step with fresh K/V):
-  do_kv_cache_update -> fused HIP kernel: rotate (MFMA) + clip + INT2 quantize
-                        + pack + paged-slot write          (kernels/quant.py)
-  _staging_write     -> HIP kernels: last writer per arena seat, owner tags,
-                        unclipped fp32 rotated window values (kernels/staging.py)
+  short steps        -> one fused step write (kernels/step.py, with the read)
+  other steps        -> do_kv_cache_update + _staging_write in one library
+                        call (kernels/quant.py): a seat-winner pass, then the
+                        fused HIP kernel: rotate (MFMA) + clip + INT2 quantize
+                        + pack + paged-slot write, whose epilogue writes the
+                        window (owner tags, unclipped fp32 rotated values and
+                        their fp16 operand images) from the same values
 Read path, per request (backend.py:273-313 routing):
   0 < q_len <= 16    -> paged MTP decode kernel over INT2 history + window
   q_len > 16         -> prefill-continuation kernel (f16 MFMA over dequantized
@@ -168,6 +171,9 @@ class OscarAttentionBackendImpl:
     # ------------------------------------------------------------------ write path
     def do_kv_cache_update(self, layer, key, value, kv_cache, slot_mapping) -> None:
         """backend.py:150-189 — rotate + clip + INT2 store of the step's tokens."""
+        self._kv_write(layer, key, value, kv_cache, slot_mapping, None)
+
+    def _kv_write(self, layer, key, value, kv_cache, slot_mapping, window) -> None:
         if key is None or value is None:
             return
         slot_mapping = slot_mapping.to(device=key.device, dtype=torch.int64)
@@ -181,9 +187,39 @@ class OscarAttentionBackendImpl:
         D = self.head_size
         quant.quant_write(key, value, op_k, op_v, self.key_cache, self.value_cache, slot_mapping,
                           quant.clip_index(cfg.k_clip_ratio, D), quant.clip_index(cfg.v_clip_ratio, D),
-                          self.num_kv_heads, D)
+                          self.num_kv_heads, D, window=window)
         self._oscar_stats["writes"] += 1
         self._oscar_stats["kv_bytes_written"] += N * self.num_kv_heads * 160
+
+    def _write_step(self, layer, key, value, kv_cache, attn_metadata) -> None:
+        """The step's INT2 write and, with the window on, its window write
+        (backend.py:277-282: do_kv_cache_update, then _staging_write) in one
+        library call: a seat-winner pass and the fused quantize-write kernel,
+        whose epilogue writes the window from the same rotated values."""
+        N = attn_metadata.num_actual_tokens
+        slot_mapping = attn_metadata.slot_mapping[:N]
+        if not self._oscar.window_enabled:
+            self.do_kv_cache_update(layer, key, value, kv_cache, slot_mapping)
+            return
+        self._ensure_staging(layer, kv_cache)
+        if N <= 0:
+            return
+        self._kv_write(layer, key, value, kv_cache, slot_mapping, self._window_args(layer, key.device, attn_metadata))
+
+    def _window_args(self, layer, dev, attn_metadata):
+        """The step's request layout and the layer's arena, as the window
+        writes take them."""
+        N = attn_metadata.num_actual_tokens
+        qsl, seqs = metadata_batch_lists(attn_metadata)
+        lengths = [max(0, min(b, N) - min(a, N)) for a, b in itertools.pairwise(qsl)]
+        if sum(lengths) != N:
+            raise ValueError("query_start_loc does not cover the step's tokens")
+        B = len(lengths)
+        meta = torch.tensor(list(qsl[:B + 1]) + list(seqs[:B]), dtype=torch.int32).to(dev, non_blocking=True)
+        _, sink_eff = self._stage_params(layer)
+        return (meta[:B + 1], meta[B + 1:], B, sink_eff, self._oscar.recent_tokens, layer._oscar_stage_k,
+                layer._oscar_stage_v, layer._oscar_slot_owner, layer._oscar_seat_winner, layer._oscar_stage_kimg,
+                layer._oscar_stage_vimg)
 
     def _ensure_staging(self, layer, kv_cache) -> None:
         """backend.py:418-437 — persistent per-layer FP32 window arena."""
@@ -199,7 +235,7 @@ class OscarAttentionBackendImpl:
         layer._oscar_stage_k = torch.zeros(rows, bs, self.num_kv_heads, self.head_size, dtype=torch.float32, device=dev)
         layer._oscar_stage_v = torch.zeros_like(layer._oscar_stage_k)
         layer._oscar_slot_owner = torch.full((rows, bs), -1, dtype=torch.int64, device=dev)
-        layer._oscar_seat_winner = torch.full((rows, bs), -1, dtype=torch.int32, device=dev)
+        layer._oscar_seat_winner = staging.winner_buffer(rows, bs, dev)
         # fp16 operand images of the window for the paged decode (32-token tiles)
         layer._oscar_stage_kimg = layer._oscar_stage_vimg = None
         if bs % 32 == 0:
@@ -224,18 +260,11 @@ class OscarAttentionBackendImpl:
         if N == 0:
             return
         dev = key.device
-        qsl, seqs = metadata_batch_lists(attn_metadata)
-        lengths = [max(0, min(b, N) - min(a, N)) for a, b in itertools.pairwise(qsl)]
-        if sum(lengths) != N:
-            raise ValueError("query_start_loc does not cover the step's tokens")
-        B = len(lengths)
-        meta = torch.tensor(list(qsl[:B + 1]) + list(seqs[:B]), dtype=torch.int32).to(dev, non_blocking=True)
+        qsl, seqs, B, sink_eff, recent, sk, sv, owner, winner, kimg, vimg = self._window_args(layer, dev, attn_metadata)
         rk, rv = self._layer_rots(layer, dev)
-        bs, sink_eff = self._stage_params(layer)
-        staging.staging_write(key, value, attn_metadata.slot_mapping[:N].to(dev), meta[:B + 1], meta[B + 1:],
-                              B, self.num_kv_heads, self.head_size, bs, sink_eff, self._oscar.recent_tokens,
-                              rk, rv, layer._oscar_stage_k, layer._oscar_stage_v, layer._oscar_slot_owner,
-                              layer._oscar_seat_winner, layer._oscar_stage_kimg, layer._oscar_stage_vimg)
+        bs, _ = self._stage_params(layer)
+        staging.staging_write(key, value, attn_metadata.slot_mapping[:N].to(dev), qsl, seqs, B, self.num_kv_heads,
+                              self.head_size, bs, sink_eff, recent, rk, rv, sk, sv, owner, winner, kimg, vimg)
 
     def _stage(self, layer):
         if self._oscar.window_enabled and getattr(layer, "_oscar_stage_ready", False):
@@ -274,11 +303,7 @@ class OscarAttentionBackendImpl:
         if self._short_step(layer, query, key, value, kv_cache, attn_metadata, output, capturing):
             self._oscar_stats["reads"] += 1
             return output
-        self.do_kv_cache_update(layer, key, value, kv_cache,
-                                attn_metadata.slot_mapping[:attn_metadata.num_actual_tokens])
-        if self._oscar.window_enabled:
-            self._ensure_staging(layer, kv_cache)
-            self._staging_write(layer, key, value, attn_metadata)
+        self._write_step(layer, key, value, kv_cache, attn_metadata)
 
         attn_out = self._read(layer, query, key, value, attn_metadata)
         self._oscar_stats["reads"] += 1

@@ -20,7 +20,12 @@
 // radix select instead (exact, slow, rare).
 //
 // Quantization: the exact divide-free thresholds of int2_quant.h.
+//
+// With a window arena (oscar_quant_write_window) the fused kernel also does
+// the window write of the step's bulk tokens from the same rotated values
+// (see window_epilogue), after a seat-winner pass over the step's slots.
 #include "int2_quant.h"
+#include "window_images.h"
 #include "../../include/oscar_amd.h"
 
 namespace oscar {
@@ -231,6 +236,84 @@ __device__ void quantize_store(const float (&v)[kPerLane], const QParams& p, int
   if (half == 0) *reinterpret_cast<uint32_t*>(kslot + 4 * side) = p.meta;
 }
 
+// The window arena of a bulk write (rows = 0: none).
+struct WindowArgs {
+  const int32_t* query_start;   // [num_requests + 1] on the device
+  const int32_t* seq_lens;      // [num_requests]
+  int32_t num_requests;
+  int32_t rows;
+  int32_t sink_eff, recent;
+  int32_t num_kv_heads;
+  float* stage_k;               // [rows][bs][Hk][D] fp32
+  float* stage_v;
+  int64_t* owner;               // [rows][bs]
+  int64_t* winner;              // seat winners (read after this call's pass)
+  _Float16* kimg;               // operand images, or null
+  _Float16* vimg;
+};
+
+// The window half of the bulk write (the reference's _staging_write,
+// backend.py:439-481) for this lane's token (slot >= 0): if the token won
+// its seat, it sets the seat's owner (the K side of head 0 does) to its page
+// when it lies in the sink or recent window and to -1 otherwise; a kept token
+// then stores this lane's 128 unclipped rotated values (features 128 half ..
+// +127 of this side and head) and their fp16 image parts.  The lane's token
+// half is exactly one lane of the K image (token row prow % 32, half g), so
+// the K parts go out as 16-byte blocks; the V image holds tokens in slots, so
+// each V value is two 2-byte stores.
+__device__ void window_epilogue(const float (&v)[kPerLane], int64_t tok, int64_t slot, int head, int side, int half,
+                                int block_size, const WindowArgs& w) {
+  int64_t seat, page;
+  if (!won_seat(w.winner, (int64_t)w.rows * block_size, slot, tok, block_size, w.rows, seat, page)) return;
+  int lo = 0, hi = w.num_requests - 1;       // request of the token: last i with query_start[i] <= tok
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (w.query_start[mid] <= tok) lo = mid; else hi = mid - 1;
+  }
+  const int64_t seq = w.seq_lens[lo];
+  const int64_t pos = seq - w.query_start[lo + 1] + tok;
+  const bool keep = pos >= seq - w.recent || pos < w.sink_eff;
+  if (side == 0 && head == 0 && half == 0) w.owner[seat] = keep ? page : -1;
+  if (!keep) return;
+  float* dst = (side == 0 ? w.stage_k : w.stage_v) + (seat * w.num_kv_heads + head) * kHeadDim + kPerLane * half;
+#pragma unroll
+  for (int k = 0; k < kPerLane / 4; ++k)
+    reinterpret_cast<floatx4*>(dst)[k] = floatx4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
+  if (w.kimg == nullptr) return;
+  const int prow = (int)(slot - page * block_size);
+  const int64_t tile = image_of(seat / block_size, prow, block_size, head, w.num_kv_heads);
+  const int tt = prow & 31;
+  if (side == 0) {
+    // block m = 2j + a, slot u = 2i + b: local feature 16j + 4a + i + 8b
+    _Float16* img = w.kimg + tile * kKImgHalfs + (tt + 32 * half) * 8;
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      half8 h, l;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float x = v[16 * (m >> 1) + 4 * (m & 1) + (u >> 1) + 8 * (u & 1)];
+        h[u] = (_Float16)x;
+        l[u] = (_Float16)(x - (float)h[u]);
+      }
+      *reinterpret_cast<half8*>(img + m * 64 * 8) = h;
+      *reinterpret_cast<half8*>(img + kImgHalfs + m * 64 * 8) = l;
+    }
+  } else {
+    _Float16* img = w.vimg + tile * kVImgHalfs;
+#pragma unroll
+    for (int k = 0; k < kPerLane; ++k) {
+      _Float16* d = img + vimg_offset(kPerLane * half + k, tt);
+      fp16_parts(v[k], d[0], d[kVPartHalfs]);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void quant_window_winner_kernel(const int64_t* __restrict__ slots, int32_t n_tokens,
+                                                                   int64_t* winner, int32_t block_size, int32_t rows) {
+  __shared__ int64_t epoch;
+  seat_winner_pass(slots, n_tokens, winner, (int64_t)rows * block_size, block_size, rows, &epoch);
+}
+
 // ---------------------------------------------------------------------------
 // Pre-rotated entry: fp32 rotated input [N, Hk, D] (token stride in elements).
 // grid = (ceil(N / 128), Hk * 2), block = 256 (4 waves x 32 tokens).
@@ -321,7 +404,8 @@ constexpr int kStaggerSleeps = 3;     // s_sleep 127 = 8128 clocks each
 __global__ __launch_bounds__(256, 2) void quant_write_fused_kernel(
     const uint16_t* __restrict__ key, const uint16_t* __restrict__ value, int64_t n_tokens,
     int64_t token_stride, const uint8_t* __restrict__ rot_k, const uint8_t* __restrict__ rot_v,
-    const int64_t* __restrict__ slots, CacheArgs c, int clip_k, int clip_v, int stagger_lo, int stagger_hi) {
+    const int64_t* __restrict__ slots, CacheArgs c, int clip_k, int clip_v, int stagger_lo, int stagger_hi,
+    WindowArgs w) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];     // ring, then the selection buffers
   {
     const int lin = blockIdx.x + gridDim.x * blockIdx.y;
@@ -428,7 +512,9 @@ __global__ __launch_bounds__(256, 2) void quant_write_fused_kernel(
   }
   SelLds& sel = reinterpret_cast<SelLds*>(ring)[wave];
   const QParams p = vector_params(v, side == 0 ? clip_k : clip_v, sel, lane);
-  quantize_store(v, p, live ? slots[tok] : -1, head, side, half, c);
+  const int64_t slot = live ? slots[tok] : -1;
+  quantize_store(v, p, slot, head, side, half, c);
+  if (w.rows > 0 && slot >= 0) window_epilogue(v, tok, slot, head, side, half, c.block_size, w);
 }
 
 // One thread per operand element (2 x 16 x 8 x 64 x 8 = 131072 entries), then
@@ -517,14 +603,17 @@ int oscar_quant_write_prerotated(const float* k_rot, const float* v_rot, int64_t
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
-int oscar_quant_write(const void* key_bf16, const void* value_bf16, int64_t num_tokens,
-                      int32_t num_kv_heads, int32_t head_size, int64_t token_stride,
-                      const void* rot_k_operand, const void* rot_v_operand,
-                      const int64_t* slot_mapping, void* k_cache, void* v_cache,
-                      int32_t block_size, int64_t num_pages, int64_t k_stride_page,
-                      int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
-                      int64_t v_stride_token, int64_t v_stride_head, int32_t clip_index_k,
-                      int32_t clip_index_v, hipStream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// oscar_quant_write with an optional window arena (w.rows > 0).
+int quant_write_impl(const void* key_bf16, const void* value_bf16, int64_t num_tokens, int32_t num_kv_heads,
+                     int32_t head_size, int64_t token_stride, const void* rot_k_operand, const void* rot_v_operand,
+                     const int64_t* slot_mapping, void* k_cache, void* v_cache, int32_t block_size,
+                     int64_t num_pages, int64_t k_stride_page, int64_t k_stride_token, int64_t k_stride_head,
+                     int64_t v_stride_page, int64_t v_stride_token, int64_t v_stride_head, int32_t clip_index_k,
+                     int32_t clip_index_v, const WindowArgs& w, hipStream_t stream) {
   if (head_size != kHeadDim) return kErrUnsupportedHeadDim;
   if (num_tokens < 0 || num_kv_heads <= 0 || clip_index_k >= kHeadDim || clip_index_v >= kHeadDim)
     return kErrInvalidArgument;
@@ -550,12 +639,14 @@ int oscar_quant_write(const void* key_bf16, const void* value_bf16, int64_t num_
   if (2 * num_tokens * num_kv_heads <= kShortWriteVectors) {
     const uint8_t* ok = static_cast<const uint8_t*>(rot_k_operand) + kMfmaOperandBytes;
     const uint8_t* ov = static_cast<const uint8_t*>(rot_v_operand) + kMfmaOperandBytes;
+    const bool win = w.rows > 0;
     return oscar_step_write(nullptr, 0, key_bf16, value_bf16, token_stride, (int32_t)num_tokens, 0, num_kv_heads,
                             head_size, reinterpret_cast<const float*>(ok), reinterpret_cast<const float*>(ov),
-                            slot_mapping, nullptr, nullptr, 0, k_cache, v_cache, block_size, num_pages,
-                            k_stride_page, k_stride_token, k_stride_head, v_stride_page, v_stride_token,
-                            v_stride_head, clip_index_k, clip_index_v, nullptr, nullptr, nullptr, nullptr,
-                            nullptr, 0, 0, 0, nullptr, nullptr, nullptr, stream);
+                            slot_mapping, win ? w.query_start : nullptr, win ? w.seq_lens : nullptr,
+                            win ? w.num_requests : 0, k_cache, v_cache, block_size, num_pages, k_stride_page,
+                            k_stride_token, k_stride_head, v_stride_page, v_stride_token, v_stride_head,
+                            clip_index_k, clip_index_v, w.stage_k, w.stage_v, w.owner, w.kimg, w.vimg, w.rows,
+                            w.sink_eff, w.recent, nullptr, nullptr, nullptr, stream);
   }
   if (set_dynamic_lds(reinterpret_cast<const void*>(quant_write_fused_kernel), (int)kFusedLds, g_lds_set) != kOk) return kErrLaunch;
   const int64_t per_block = kFusedWaves * kTokPerWave;
@@ -571,12 +662,65 @@ int oscar_quant_write(const void* key_bf16, const void* value_bf16, int64_t num_
   const bool stagger = blocks >= 4 * (int64_t)cus && (clip_index_k >= 0 || clip_index_v >= 0);
   const int lo = stagger ? cus : 0;
   const int hi = stagger ? 2 * cus : 0;
+  if (w.rows > 0) {
+    hipLaunchKernelGGL(quant_window_winner_kernel, dim3((unsigned)((num_tokens + 255) / 256)), dim3(256), 0, stream,
+                       slot_mapping, (int32_t)num_tokens, w.winner, block_size, w.rows);
+    if (hipGetLastError() != hipSuccess) return kErrLaunch;
+  }
   hipLaunchKernelGGL(quant_write_fused_kernel, grid, dim3(kFusedWaves * 64), kFusedLds, stream,
                      static_cast<const uint16_t*>(key_bf16), static_cast<const uint16_t*>(value_bf16),
                      num_tokens, token_stride, static_cast<const uint8_t*>(rot_k_operand),
                      static_cast<const uint8_t*>(rot_v_operand), slot_mapping, c,
-                     (int)clip_index_k, (int)clip_index_v, lo, hi);
+                     (int)clip_index_k, (int)clip_index_v, lo, hi, w);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+}  // namespace
+
+extern "C" {
+
+int oscar_quant_write(const void* key_bf16, const void* value_bf16, int64_t num_tokens,
+                      int32_t num_kv_heads, int32_t head_size, int64_t token_stride,
+                      const void* rot_k_operand, const void* rot_v_operand,
+                      const int64_t* slot_mapping, void* k_cache, void* v_cache,
+                      int32_t block_size, int64_t num_pages, int64_t k_stride_page,
+                      int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
+                      int64_t v_stride_token, int64_t v_stride_head, int32_t clip_index_k,
+                      int32_t clip_index_v, hipStream_t stream) {
+  return quant_write_impl(key_bf16, value_bf16, num_tokens, num_kv_heads, head_size, token_stride, rot_k_operand,
+                          rot_v_operand, slot_mapping, k_cache, v_cache, block_size, num_pages, k_stride_page,
+                          k_stride_token, k_stride_head, v_stride_page, v_stride_token, v_stride_head,
+                          clip_index_k, clip_index_v, WindowArgs{}, stream);
+}
+
+int oscar_quant_write_window(const void* key_bf16, const void* value_bf16, int64_t num_tokens,
+                             int32_t num_kv_heads, int32_t head_size, int64_t token_stride,
+                             const void* rot_k_operand, const void* rot_v_operand,
+                             const int64_t* slot_mapping, void* k_cache, void* v_cache,
+                             int32_t block_size, int64_t num_pages, int64_t k_stride_page,
+                             int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_page,
+                             int64_t v_stride_token, int64_t v_stride_head, int32_t clip_index_k,
+                             int32_t clip_index_v, const int32_t* query_start_loc, const int32_t* seq_lens,
+                             int32_t num_requests, int32_t stage_rows, int32_t sink_eff, int32_t recent,
+                             float* stage_k, float* stage_v, int64_t* stage_owner, int64_t* seat_winner,
+                             void* stage_k_image, void* stage_v_image, hipStream_t stream) {
+  if (num_requests < 0 || stage_rows <= 0 || sink_eff < 0 || recent < 0 || num_tokens > INT32_MAX)
+    return kErrInvalidArgument;
+  if (num_tokens > 0 && num_requests == 0) return kErrInvalidArgument;
+  if (!query_start_loc || !seq_lens || !stage_k || !stage_v || !stage_owner || !seat_winner)
+    return kErrInvalidArgument;
+  if ((stage_k_image == nullptr) != (stage_v_image == nullptr)) return kErrInvalidArgument;
+  if (stage_k_image != nullptr && block_size % 32 != 0) return kErrUnsupportedGeometry;
+  if ((reinterpret_cast<uintptr_t>(stage_k) & 15) || (reinterpret_cast<uintptr_t>(stage_v) & 15) ||
+      (reinterpret_cast<uintptr_t>(stage_k_image) & 15) || (reinterpret_cast<uintptr_t>(stage_v_image) & 15))
+    return kErrInvalidArgument;
+  WindowArgs w{query_start_loc, seq_lens, num_requests, stage_rows, sink_eff, recent, num_kv_heads, stage_k, stage_v,
+               stage_owner, seat_winner, static_cast<_Float16*>(stage_k_image),
+               static_cast<_Float16*>(stage_v_image)};
+  return quant_write_impl(key_bf16, value_bf16, num_tokens, num_kv_heads, head_size, token_stride, rot_k_operand,
+                          rot_v_operand, slot_mapping, k_cache, v_cache, block_size, num_pages, k_stride_page,
+                          k_stride_token, k_stride_head, v_stride_page, v_stride_token, v_stride_head,
+                          clip_index_k, clip_index_v, w, stream);
 }
 
 }  // extern "C"

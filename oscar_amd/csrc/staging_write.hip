@@ -8,9 +8,10 @@
 // the winner sets owner[seat] = s / bs if kept, else -1, and a kept winner
 // stores its unclipped rotated K/V (x @ R, fp32) in the seat.
 //
-// Kernel 1 records the winning token index per seat with atomicMax into a
-// persistent int32 array that starts (and is left) at -1.  Kernel 2: one block
-// per token; the winner updates owner / values and resets its seat to -1.
+// Kernel 1 records the winning token per seat with a 64-bit atomicMax of
+// epoch-tagged keys into a persistent buffer that is never reset (see
+// seat_winner_pass).  Kernel 2: one block per token; the winner updates
+// owner / values.
 //
 // A kept winner also refreshes the fp16 operand images of window_images.h.
 #include "window_images.h"
@@ -37,22 +38,14 @@ struct StageArgs {
   float* stage_k;           // [rows][bs][Hk][D]
   float* stage_v;
   int64_t* owner;           // [rows][bs]
-  int32_t* winner;          // [rows][bs], -1 between calls
+  int64_t* winner;          // [rows * bs] keys, then epoch and arrival counter
   _Float16* kimg;           // [rows][bs / 32][Hk][kKImgHalfs] or null
   _Float16* vimg;           // [rows][bs / 32][Hk][kVImgHalfs] or null
 };
 
-__device__ __forceinline__ int64_t seat_of(int64_t slot, const StageArgs& a) {
-  const int64_t page = slot / a.block_size;
-  return (page % a.rows) * a.block_size + (slot - page * a.block_size);
-}
-
-__global__ void stage_winner_kernel(StageArgs a) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= a.n_tokens) return;
-  const int64_t s = a.slots[t];
-  if (s < 0) return;
-  atomicMax(a.winner + seat_of(s, a), t);
+__global__ __launch_bounds__(256) void stage_winner_kernel(StageArgs a) {
+  __shared__ int64_t epoch;
+  seat_winner_pass(a.slots, a.n_tokens, a.winner, (int64_t)a.rows * a.block_size, a.block_size, a.rows, &epoch);
 }
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t x) {
@@ -65,8 +58,9 @@ __global__ __launch_bounds__(256) void stage_update_kernel(StageArgs a) {
   const int t = blockIdx.x;
   const int64_t s = a.slots[t];
   if (s < 0) return;
-  const int64_t seat = seat_of(s, a);
-  if (a.winner[seat] != t) return;       // block-uniform
+  int64_t seat, page;
+  if (!won_seat(a.winner, (int64_t)a.rows * a.block_size, s, t, a.block_size, a.rows, seat, page))
+    return;                              // block-uniform
   // Request of token t: last i with query_start[i] <= t.
   int lo = 0, hi = a.num_requests - 1;
   while (lo < hi) {
@@ -77,10 +71,7 @@ __global__ __launch_bounds__(256) void stage_update_kernel(StageArgs a) {
   const int64_t pos = seq - a.query_start[lo + 1] + t;
   const bool keep = pos >= seq - a.recent || pos < a.sink_eff;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    a.owner[seat] = keep ? s / a.block_size : -1;
-    a.winner[seat] = -1;
-  }
+  if (threadIdx.x == 0) a.owner[seat] = keep ? page : -1;
   if (!keep) return;
   const int f = threadIdx.x;
   for (int h = 0; h < a.num_kv_heads; ++h) {
@@ -121,7 +112,7 @@ extern "C" int oscar_staging_write(const void* key_bf16, const void* value_bf16,
                                    int32_t block_size, int32_t stage_rows, int32_t sink_eff,
                                    int32_t recent, const float* rot_k, const float* rot_v,
                                    float* stage_k, float* stage_v, int64_t* stage_owner,
-                                   int32_t* seat_winner, void* stage_k_image, void* stage_v_image,
+                                   int64_t* seat_winner, void* stage_k_image, void* stage_v_image,
                                    hipStream_t stream) {
   if (head_size != kHeadDim) return kErrUnsupportedHeadDim;
   if (num_tokens < 0 || num_requests < 0 || num_kv_heads <= 0 || block_size <= 0 || stage_rows <= 0 ||

@@ -54,4 +54,52 @@ __device__ __forceinline__ int64_t image_of(int64_t arow, int prow, int block_si
   return (arow * (block_size / 32) + prow / 32) * num_kv_heads + h;
 }
 
+// Seat winners of a bulk window write.  The buffer is int64
+// [seats + 2]: one key per arena seat, then the epoch of the last call and an
+// arrival counter (all zero when allocated; never reset).  A call's pass over
+// its tokens stores max(key, (epoch + 1) << 32 | t) per seat (t: token index
+// within the step), and its last workgroup to arrive advances the epoch, so
+// that afterwards a seat's winner is the token t whose key equals
+// epoch << 32 | t.  Keys of earlier calls carry smaller epochs and lose.
+__device__ __forceinline__ int64_t winner_key(int64_t epoch, int64_t t) { return (epoch << 32) | t; }
+
+// One thread per token of the pass (blockDim.x threads per workgroup).
+__device__ __forceinline__ void seat_winner_pass(const int64_t* __restrict__ slots, int32_t n_tokens, int64_t* winner,
+                                                 int64_t seats, int32_t block_size, int32_t rows, int64_t* epoch_lds) {
+  if (threadIdx.x == 0)
+    *epoch_lds = __hip_atomic_load(winner + seats, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+  __syncthreads();
+  const int64_t e = *epoch_lds;
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < n_tokens) {
+    const int64_t s = slots[t];
+    if (s >= 0) {
+      const int64_t page = s / block_size;
+      const int64_t seat = (page % rows) * block_size + (s - page * block_size);
+      __hip_atomic_fetch_max(reinterpret_cast<unsigned long long*>(winner + seat),
+                             (unsigned long long)winner_key(e, t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    // every thread of this workgroup has read the epoch; the last workgroup
+    // to arrive publishes the call's epoch and clears the counter
+    const unsigned long long done = __hip_atomic_fetch_add(reinterpret_cast<unsigned long long*>(winner + seats + 1),
+                                                           1ull, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (done == gridDim.x - 1) {
+      __hip_atomic_store(winner + seats, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(winner + seats + 1, (int64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// After the pass (a later launch): whether token t with slot s (>= 0) won
+// its seat; seat returned.
+__device__ __forceinline__ bool won_seat(const int64_t* winner, int64_t seats, int64_t s, int64_t t, int32_t block_size,
+                                         int32_t rows, int64_t& seat, int64_t& page) {
+  page = s / block_size;
+  seat = (page % rows) * block_size + (s - page * block_size);
+  return winner[seat] == winner_key(winner[seats], t);
+}
+
 }  // namespace oscar

@@ -8,7 +8,7 @@ whole cache blocks.  Per OSCAR layer the fixed buffers here are
   * the FP32 window arena                      rows * bs * (2 * Hk * D * 4 + 8)
   * its fp16 MFMA operand images (high and    rows * bs * 4 * Hk * D * 2
     low parts of K and of V)
-  * the arena's seat-winner scratch            rows * bs * 4
+  * the arena's seat-winner buffer             rows * bs * 8 + 16
 and, once per device, the split-decode workspace of the largest batch and
 the library's no-allocation decode array (32 MiB, a static device array every
 GPU that loads the library holds whether or not that entry is called).
@@ -50,7 +50,7 @@ def fixed_bytes_per_layer(head_dim: int, num_kv_heads: int, block_size: int, sin
     fixed = 4 * head_dim * head_dim * 4 + 2 * ROTATION_OPERAND_BYTES
     if window:
         rows = arena_rows(block_size, sink, recent, staging)
-        fixed += rows * block_size * (2 * num_kv_heads * head_dim * 4 + 4 * num_kv_heads * head_dim * 2 + 8 + 4)
+        fixed += rows * block_size * (2 * num_kv_heads * head_dim * 4 + 4 * num_kv_heads * head_dim * 2 + 8 + 8) + 16
     return fixed
 
 

@@ -61,6 +61,10 @@ SIGNATURES = {
     "oscar_staging_write": (_c_i32, [_c_p, _c_p, _c_i64, _c_p, _c_i32, _c_p, _c_p, _c_i32, _c_i32,
                                      _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p,
                                      _c_p, _c_p, _c_p, _c_p, _c_p]),
+    "oscar_quant_write_window": (_c_i32, [_c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i64, _c_p, _c_p, _c_p,
+                                          _c_p, _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                          _c_i64, _c_i64, _c_i32, _c_i32, _c_p, _c_p, _c_i32, _c_i32, _c_i32,
+                                          _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
 }
 
 STATUS = {

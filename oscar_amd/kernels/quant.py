@@ -9,7 +9,7 @@ from __future__ import annotations
 import torch
 
 from ..format import HEAD_DIM, check_d
-from . import _lib
+from . import _lib, staging
 
 
 def clip_index(ratio: float, D: int) -> int:
@@ -83,9 +83,14 @@ def quant_write_prerotated(k_rot, v_rot, k_cache, v_cache, slot_mapping, clip_k:
 
 
 def quant_write(key, value, rot_k_op, rot_v_op, k_cache, v_cache, slot_mapping, clip_k: int,
-                clip_v: int, num_kv_heads: int, head_size: int) -> None:
+                clip_v: int, num_kv_heads: int, head_size: int, window=None) -> None:
     """Fused rotate + clip + quantize + pack + write of bf16 K/V: the rotation
-    runs on MFMA, or in fp32 for writes of at most 2048 key + value vectors."""
+    runs on MFMA, or in fp32 for writes of at most 2048 key + value vectors.
+    window: None, or (query_start, seq_lens, num_requests, sink_eff, recent,
+    stage_k, stage_v, owner, winner, k_image, v_image) -- the step's request
+    layout (int32 device tensors) and the window arena, whose write (the
+    reference's _staging_write, backend.py:439-481) then comes from the same
+    rotated values in the same call."""
     N = slot_mapping.shape[0]
     if N == 0:
         return
@@ -99,6 +104,18 @@ def quant_write(key, value, rot_k_op, rot_v_op, k_cache, v_cache, slot_mapping, 
         ks = kr.stride(0)
     slots = slot_mapping.to(torch.int64).contiguous()
     bs, pages, kst, vst = cache_geometry(k_cache, v_cache)
-    _lib.call("oscar_quant_write", _lib.ptr(kr), _lib.ptr(vr), N, hk, D, ks, _lib.ptr(rot_k_op),
-              _lib.ptr(rot_v_op), _lib.ptr(slots), _lib.ptr(k_cache), _lib.ptr(v_cache), bs,
-              pages, *kst, *vst, clip_k, clip_v, _lib.stream_handle(key.device))
+    common = (_lib.ptr(kr), _lib.ptr(vr), N, hk, D, ks, _lib.ptr(rot_k_op), _lib.ptr(rot_v_op), _lib.ptr(slots),
+              _lib.ptr(k_cache), _lib.ptr(v_cache), bs, pages, *kst, *vst, clip_k, clip_v)
+    if window is None:
+        _lib.call("oscar_quant_write", *common, _lib.stream_handle(key.device))
+        return
+    qsl, seqs, B, sink_eff, recent, sk, sv, owner, winner, kimg, vimg = window
+    rows = staging.check_arena(sk, sv, owner, bs, hk, D)
+    staging.check_images(kimg, vimg, rows, bs, hk)
+    staging.check_winner(winner, rows, bs)
+    for t in (qsl, seqs):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise ValueError("the request layout must be contiguous int32 device tensors")
+    _lib.call("oscar_quant_write_window", *common, _lib.ptr(qsl), _lib.ptr(seqs), B, rows, sink_eff, recent,
+              _lib.ptr(sk), _lib.ptr(sv), _lib.ptr(owner), _lib.ptr(winner), _lib.ptr(kimg), _lib.ptr(vimg),
+              _lib.stream_handle(key.device))

@@ -64,6 +64,19 @@ def check_arena(stage_k, stage_v, owner, bs: int, hk: int, d: int) -> int:
     return rows
 
 
+def winner_buffer(rows: int, bs: int, device) -> torch.Tensor:
+    """The seat-winner buffer of an arena's bulk writes: int64, one key per
+    seat, then the call epoch and an arrival counter; zero once, kept across
+    calls (the kernels never need it reset)."""
+    return torch.zeros(rows * bs + 2, dtype=torch.int64, device=device)
+
+
+def check_winner(winner, rows: int, bs: int) -> None:
+    if winner is None or winner.dtype != torch.int64 or winner.ndim != 1 or winner.numel() != rows * bs + 2 \
+            or not winner.is_contiguous():
+        raise ValueError(f"seat winners must be a contiguous int64 [{rows * bs + 2}] buffer (winner_buffer)")
+
+
 def check_images(k_image, v_image, rows: int, bs: int, hk: int) -> None:
     """Raise unless the operand images are absent together or are contiguous
     fp16 tensors of the arena's K and V image shapes (the kernels index them
@@ -121,6 +134,7 @@ def staging_write(key, value, slot_mapping, qsl_dev, seq_dev, num_requests: int,
     slots = slot_mapping.to(torch.int64).contiguous()
     check_arena(stage_k, stage_v, owner, block_size, num_kv_heads, head_size)
     check_images(k_image, v_image, owner.shape[0], block_size, num_kv_heads)
+    check_winner(winner, owner.shape[0], block_size)
     _lib.call("oscar_staging_write", _lib.ptr(kr), _lib.ptr(vr), kr.stride(0), _lib.ptr(slots), N,
               _lib.ptr(qsl_dev), _lib.ptr(seq_dev), num_requests, num_kv_heads, head_size, block_size,
               owner.shape[0], sink_eff, recent, _lib.ptr(R_k), _lib.ptr(R_v), _lib.ptr(stage_k),

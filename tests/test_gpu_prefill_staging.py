@@ -3,6 +3,12 @@
 * Window write: owner tags bit-exact with the oracle arena
   (restating oscar_ascend/backend.py:439-481); staged fp32 values within
   1e-5 relative of the oracle's fp32 CPU rotation (summation order differs).
+* The bulk step write with the window fused in (seat-winner pass + the
+  quantize-write kernel's window epilogue): owner tags bit-exact, operand
+  images bit-exact with the staged values, INT2 caches bit-identical to the
+  window-less write; staged values are the MFMA rotation with R split into
+  bf16 high + low parts (R carried to 2^-18 of each entry), within 1e-4 of
+  the values' scale of the oracle's fp32 rotation.
 * Prefill continuation: against the oracle dense path (history dequant +
   window splice + causal SDPA, restating backend.py:361-415 and
   kernels/decode_kernel.py:70-117) evaluated in fp32, as the reference's own
@@ -19,7 +25,7 @@ from oracle import attention as oatt
 from oracle import store as ostore
 from oracle.staging import Arena
 from oscar_amd import synthetic
-from oscar_amd.kernels import prefill, staging
+from oscar_amd.kernels import prefill, quant, staging
 from tests.scenarios import decode_case, metadata
 
 pytestmark = pytest.mark.gpu
@@ -30,7 +36,7 @@ def _gpu_arena(arena, device):
     sk = torch.zeros_like(arena.stage_k, device=device)
     sv = torch.zeros_like(sk)
     owner = torch.full(arena.owner.shape, -1, dtype=torch.int64, device=device)
-    winner = torch.full(arena.owner.shape, -1, dtype=torch.int32, device=device)
+    winner = staging.winner_buffer(arena.rows, arena.bs, device)
     kimg = vimg = None
     if arena.bs % 32 == 0:
         geom = (arena.rows, arena.bs, arena.stage_k.shape[2])
@@ -83,11 +89,59 @@ def test_window_write_matches_oracle_over_steps(device, bs, sink, recent, stagin
             # The fp16 operand images track the fp32 arena exactly (same RNE cast).
             kref, vref = staging.stage_images(gpu[0], gpu[1])
             assert torch.equal(gpu[4], kref) and torch.equal(gpu[5], vref), f"operand images differ at step {i}"
-        assert (winner == -1).all()
+        assert winner[-2].item() == i + 1 and winner[-1].item() == 0     # one epoch per call, counter cleared
         live = arena.owner >= 0
         for got, want in ((sk, arena.stage_k), (sv, arena.stage_v)):
             err = (got[live] - want[live]).abs().max().item() if live.any() else 0.0
             assert err <= 1e-5 * max(1.0, want[live].abs().max().item()), err
+
+
+@pytest.mark.parametrize("bs,sink,recent,staging_tokens,hk", [(16, 16, 32, 64, 1), (128, 128, 256, 2048, 2)])
+def test_fused_bulk_window_write_matches_oracle(device, bs, sink, recent, staging_tokens, hk):
+    Rk, Rv = synthetic.rotations(D, seed=33)
+    op_k, op_v = quant.rotation_operand(Rk.to(device)), quant.rotation_operand(Rv.to(device))
+    clip_k, clip_v = quant.clip_index(0.96, D), quant.clip_index(0.92, D)
+    arena = Arena.create(bs, hk, D, sink, recent, staging_tokens)
+    gpu = _gpu_arena(arena, device)
+    g = torch.Generator().manual_seed(11)
+    pages = 4 * (2400 // bs + 2)
+    caches_w = [torch.zeros(pages, bs, hk, D, dtype=torch.int8, device=device) for _ in range(2)]
+    caches_p = [torch.zeros_like(c) for c in caches_w]
+    perm = torch.randperm(pages, generator=g).to(torch.int32)
+    T = pages // 4
+    bt = torch.stack([perm[:T], perm[T:2 * T]])
+    # Step 1: two prefills of 1500 + 700 tokens (fused path; pages collide in
+    # the arena's few rows), step 2: a 4 + 4-token step (short path), step 3:
+    # a 1200-token prefill over the first request's pages in reverse order.
+    h0, h1 = 1500, 700
+    steps = [(torch.cat([synthetic.slots_for(bt[0], 0, h0, bs), synthetic.slots_for(bt[1], 0, h1, bs)]),
+              [0, h0, h0 + h1], [h0, h1]),
+             (torch.cat([synthetic.slots_for(bt[0], h0, 4, bs), synthetic.slots_for(bt[1], h1, 4, bs)]),
+              [0, 4, 8], [h0 + 4, h1 + 4]),
+             (synthetic.slots_for(bt[0].flip(0), 0, 1200, bs), [0, 1200], [1200])]
+    steps[0][0][17] = -1                       # a skipped slot inside the fused step
+    for i, (slots, qsl, seqs) in enumerate(steps):
+        k, v = synthetic.kv(slots.numel(), hk, D, seed=50 + i)
+        md = metadata(slots, qsl, seqs, bt)
+        arena.write(k, v, md, Rk, Rv)
+        B = len(seqs)
+        meta = torch.tensor(qsl + seqs, dtype=torch.int32, device=device)
+        kd, vd, sd = k.to(device), v.to(device), slots.to(device)
+        window = (meta[:B + 1], meta[B + 1:], B, arena.sink_eff, arena.recent, *gpu)
+        quant.quant_write(kd, vd, op_k, op_v, caches_w[0], caches_w[1], sd, clip_k, clip_v, hk, D, window=window)
+        quant.quant_write(kd, vd, op_k, op_v, caches_p[0], caches_p[1], sd, clip_k, clip_v, hk, D)
+        torch.cuda.synchronize()
+        sk, sv, owner = (t.cpu() for t in gpu[:3])
+        assert torch.equal(owner, arena.owner), f"owner tags differ at step {i}"
+        if gpu[4] is not None:                 # images exist for block sizes that are multiples of 32
+            kref, vref = staging.stage_images(gpu[0], gpu[1])
+            assert torch.equal(gpu[4], kref) and torch.equal(gpu[5], vref), f"operand images differ at step {i}"
+        assert torch.equal(caches_w[0], caches_p[0]) and torch.equal(caches_w[1], caches_p[1])
+        live = arena.owner >= 0
+        assert live.any()
+        for got, want in ((sk, arena.stage_k), (sv, arena.stage_v)):
+            err = (got[live] - want[live]).abs().max().item()
+            assert err <= 1e-4 * max(1.0, want[live].abs().max().item()), (i, err)
 
 
 @pytest.mark.parametrize("window", [False, True])
