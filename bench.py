@@ -25,6 +25,11 @@ Also in the line (config):
   long-context decode through the MTP and DecodeOnly entries, and the
   15360 + 9256 prefill continuation.
 
+roofline.traffic (HBM bytes per call) and mfma_util come from the committed
+rocprofv3 summaries profiles/hbm_traffic.txt and profiles/mfma_counters.txt,
+and only while every source file they were measured on is unchanged (each
+summary records their sha256); otherwise they are null.
+
 cpu_baseline: the CPU oracle's forward of the same step (rotate + clip +
 INT2 write + window write of the 4 new tokens, then history dequant + window
 splice + causal SDPA + output rotation, fp32) on this host's cores, and at 2
@@ -414,22 +419,41 @@ def copy_probe(dev, mib: int) -> None:
     log(f"bench: copy probe {mib} MiB x 4")
 
 
-def traffic_from_profile(kernel_src: Path):
-    """HBM bytes per decode call from the committed PMC summary, if it was
-    measured on the current kernel source (sha256 recorded in the summary)."""
+def profile_figures(name: str) -> dict:
+    """The figures of a committed rocprofv3 summary (profiles/<name>, lines
+    'figure <key>: <value>'), if every source it was measured on (lines
+    'source_sha256 <file under oscar_amd/csrc>: <hex>') is unchanged; else {}
+    (the bench then reports those figures as null)."""
     import hashlib
 
-    prof = ROOT / "profiles" / "decode_c2_traffic.txt"
+    prof = ROOT / "profiles" / name
     if not prof.exists():
-        return None
-    fields = dict(l.split(":", 1) for l in prof.read_text().splitlines() if ":" in l and not l.startswith(" "))
-    digest = hashlib.sha256(kernel_src.read_bytes()).hexdigest()
-    if fields.get("source_sha256", "").strip() != digest:
-        return None
-    try:
-        return int(fields["traffic_bytes_per_call"].strip())
-    except (KeyError, ValueError):
-        return None
+        return {}
+    figs, sources = {}, 0
+    for line in prof.read_text().splitlines():
+        if ":" not in line or line.startswith(" "):
+            continue
+        key, val = (x.strip() for x in line.split(":", 1))
+        if key.startswith("source_sha256 "):
+            src = ROOT / "oscar_amd" / "csrc" / key.split(" ", 1)[1]
+            if not src.exists() or hashlib.sha256(src.read_bytes()).hexdigest() != val:
+                return {}
+            sources += 1
+        elif key.startswith("figure "):
+            try:
+                figs[key.split(" ", 1)[1]] = float(val)
+            except ValueError:
+                pass
+    return figs if sources else {}
+
+
+def _traffic(key: str):
+    v = profile_figures("hbm_traffic.txt").get(f"traffic {key}")
+    return None if v is None else int(v)
+
+
+def _mfma(key: str):
+    return profile_figures("mfma_counters.txt").get(f"mfma_util {key}")
 
 
 # ---------------------------------------------------------------- CPU oracle
@@ -636,7 +660,9 @@ def suite(dev, names, cpu_seconds, steps=8):
                          "arith": "bf16 contract: INT2 codes as exact f16 operands, f16 MFMA, f32 softmax",
                          "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1),
                                       "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                      "frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4), "flops": r["flops"]},
+                                      "frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4), "flops": r["flops"],
+                                      "traffic": _traffic("C4")},
+                         "mfma_util": _mfma("C4"),
                          "parity_max_abs_err": err, "cpu_baseline": cpu}
             continue
         only = cfg.get("decode_only", False)
@@ -654,7 +680,7 @@ def suite(dev, names, cpu_seconds, steps=8):
                      "steps": steps, "layers_per_step": len(states), "calls_timed": steps * len(states),
                      "roofline": {"bound": "hbm", "achieved": round(dec["gbps"], 1), "peak": HBM_PEAK_GBPS,
                                   "unit": "GB/s", "frac": round(dec["gbps"] / HBM_PEAK_GBPS, 4),
-                                  "bytes_per_layer": dec["bytes"]["total"]},
+                                  "bytes_per_layer": dec["bytes"]["total"], "traffic": _traffic(name)},
                      "staged_tokens": dec["bytes"]["staged_tokens"], "parity_rel_err": rel, "cpu_baseline": cpu}
     return out
 
@@ -756,6 +782,7 @@ def main():
                 "states": "4 distinct inputs and caches (4 x ~55 MB), one call each per step",
                 "us_per_call": round(qw["us"], 3), "gbps": round(qw["gbps"], 1),
                 "frac_of_hbm_peak": round(qw["gbps"] / HBM_PEAK_GBPS, 4), "bytes_per_call": qw["bytes"],
+                "traffic": _traffic("quant_write"), "mfma_util": _mfma("quant_write"),
                 "short_write_us": qw["short_us"],
                 "short_write": "us per call of 4- and 64-token writes (same caches and clip), the fp32 "
                                "short path"},
@@ -763,7 +790,7 @@ def main():
         },
         "roofline": {"bound": "hbm", "achieved": round(dec["gbps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(dec["gbps"] / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic_from_profile(ROOT / "oscar_amd" / "csrc" / "paged_decode.hip")},
+                     "traffic": _traffic("C2")},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -478,3 +478,24 @@ def test_short_step_routing_and_capture(clean_env, monkeypatch):
     assert impl._short_step(layer, q, k, k, c, md, out, False) is True
     assert impl._short_step(layer, q, k, k, c, md, out, False) is True
     assert len(built) == 3 and fake.calls[2]["step"] == fake.calls[3]["step"]
+
+
+def test_bench_profile_figures_need_unchanged_sources(tmp_path, monkeypatch):
+    """bench.py reports a committed rocprofv3 figure only while every source it
+    was measured on hashes as recorded; a changed source turns it into null."""
+    import hashlib
+
+    import bench
+
+    src = tmp_path / "oscar_amd" / "csrc"
+    src.mkdir(parents=True)
+    (src / "k.hip").write_text("kernel v1\n")
+    (tmp_path / "profiles").mkdir()
+    digest = hashlib.sha256(b"kernel v1\n").hexdigest()
+    (tmp_path / "profiles" / "t.txt").write_text(
+        f"header line: not a figure\nfigure traffic C2: 1234\nsource_sha256 k.hip: {digest}\n")
+    monkeypatch.setattr(bench, "ROOT", tmp_path)
+    assert bench.profile_figures("t.txt") == {"traffic C2": 1234.0}
+    (src / "k.hip").write_text("kernel v2\n")
+    assert bench.profile_figures("t.txt") == {}
+    assert bench.profile_figures("missing.txt") == {}
