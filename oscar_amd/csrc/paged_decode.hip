@@ -12,44 +12,55 @@
 // per row tile, so each INT2 token is read and unpacked once for all of them.
 // A work item is (request, kv head, row tile).
 //
-// split kernel, grid (S + 1, items, row tiles), 4 wavefronts per workgroup:
-//  * workgroup s < S: history split s.  Wave w takes the 32-token tiles
-//    s + S (w + 4k) of the history, so the window's tiles (first and last
-//    pages) spread over many waves.  The query rows and the wave's pages are
-//    requested before anything is waited for, then the first two tiles' codes,
-//    meta and owner tags; tiles are double-buffered after that.
-//    Per tile (one page, as block_size % 32 == 0):
-//    * S^T = K Q^T on 32x32x16 f16 MFMA.  K operands are the exact fp16 values
-//      1 + c/4 built from the code bits (one shift and one and-or per pair);
-//      the token's scale s and zero z act on the score tile:
-//        q.k = s * sum q c + z * sum q = 4s * (q.k') + (z - 4s) * sum q.
-//      The K dimension is permuted (feature 128g + 16j + 4a + i + 8b sits in
-//      k-step 2j + a, slot 2i + b) so that pairs come straight out of a code
-//      dword; Q^T (fp16, in LDS) uses the same permutation.
-//    * O^T += V^T P'^T on 16 more MFMAs with V operands 1 + c/4 from byte-
-//      transposed codes in LDS and P' = p * vs (fp16).  Then
-//        sum_t p (c vs + vz) = 4 * acc - 4 * sum_t P' + sum_t p vz,
-//      where sum_t P' is taken over the same fp16 values (v_dot2).
-//    * Tokens owned by the staging arena are masked out of that pass.  The
-//      first tile of a wave that holds any has its fp16 operand images (K in
-//      the MFMA A-operand lane order, V^T likewise) copied to LDS with
-//      global_load_lds_dwordx4 as soon as its owner tags arrive, and is run
-//      again from the images after the INT2 tiles, for its window tokens only
-//      (probabilities enter the PV pass as p / 4).  Further such tiles of the
-//      same wave (common only when the window holds long-decoded history) are
-//      run from their images one by one afterwards.
-//    Base-2 online softmax in fp32; a row's running max is only raised when a
-//    tile's max exceeds it by more than 2^4 (so P' <= 16 * vs stays finite in
-//    fp16; a tile with a V scale above 4094 raises it eagerly), and the first
-//    raise of a row needs no rescale.  The 4 wavefronts agree on a common max
-//    in LDS and reduce-scatter their O^T fragments in two LDS rounds: wave w
-//    ends with features 64w .. 64w + 63 of every row, transposes them through
-//    LDS and writes whole row segments of the split's partial [32 rows][256]
-//    + m[32] + l[32] (fp32, row-major).
-//  * workgroup S: the step's own new tokens in exact fp32 (row (token j,
-//    head) against new tokens 0 .. j), written as one more partial.
-// merge kernel: one 256-thread block per (output row, feature quarter) of an
-//   item; LSE-combines the item's partials and writes that slice of the row.
+// History splits: an item's history is cut into 128-token steps (one 32-token
+// tile per wavefront); split s of an item with S splits takes steps s,
+// s + S, s + 2S, ..., so the window's first and last steps land in different
+// workgroups.  The host plans S per item (a common number of steps per split,
+// the smallest that keeps the launch's splits within one round of resident
+// workgroups).  The grid's x dimension runs over the launch chunk's
+// workgroups: each item's splits (split 0 first, then S - 1, S - 2, ..., 1,
+// so that the window steps start first), then the item's fresh-token
+// workgroup when it has one; a workgroup finds its item by a binary search
+// of the items' first workgroups.  The z dimension is the row tile.
+//
+// split kernels (4 wavefronts, two workgroups per CU), one fp32 partial
+// [32 rows][256] + m[32] + l[32] per (item, split, row tile):
+//  * paged_decode_split_kernel (items of more than 8 rows): the wavefronts
+//    take a step together.  Wave w scores tile w of the step for every row:
+//    S^T = K Q^T on 32x32x16 f16 MFMA.  K operands are the exact fp16 values
+//    1 + c/4 built from the code bits (one shift and one and-or per pair);
+//    the token's scale s and zero z act on the score tile:
+//      q.k = s * sum q c + z * sum q = 4s * (q.k') + (z - 4s) * sum q.
+//    The K dimension is permuted (feature 128g + 16j + 4a + i + 8b sits in
+//    k-step 2j + a, slot 2i + b) so that pairs come straight out of a code
+//    dword; Q^T sits in LDS as an fp16 high part and low part (q - high),
+//    and each K operand meets both.  The waves agree on the step's row maxima
+//    in LDS and write P' = p * vs (fp16) of their tiles there; wave w then
+//    accumulates features 64w .. 64w + 63 of every row over the step's four
+//    tiles, O^T += V^T P'^T with V operands 1 + c/4 from byte-transposed
+//    codes, and
+//      sum_t p (c vs + vz) = 4 * acc - 4 * sum_t P' + sum_t p vz.
+//    Window-owned tokens (arena owner tag = the token's page) take their K
+//    operand from the tile's fp16 image (high part, then the low part against
+//    q's high part) and their V from the V image's high and low parts, with
+//    weight p / 4.
+//  * paged_decode_split_small_kernel (items of at most 8 rows): each
+//    wavefront walks its own tiles on 16x16x32 MFMA tiles (its own comment
+//    below).
+//  Base-2 online softmax in fp32; a row's running max is raised only when a
+//  tile or step exceeds it by more than 2^kLazy (so P' = p * vs stays finite
+//  in fp16; a V scale above kLazyVsMax raises it eagerly), and the first
+//  raise of a row needs no rescale.  Every row sum is taken over the weights
+//  as their fp16 rounding left them, so the output stays a convex
+//  combination of the values.
+//  * the fresh-token workgroup of an item (or, when the item has none of its
+//    own, the history split with the least work): the step's own new tokens
+//    in exact fp32 (row (token j, head) against new tokens 0 .. j), written
+//    as one more partial.
+// merge kernels: the item's partials LSE-combined per output row (one block
+//   per row and feature quarter, or one thread per four features when every
+//   item has at most 32 partials); the rotated variant also multiplies by
+//   R_v^T and casts to the output dtype.
 //
 // DecodeOnly read (no fresh K/V; one query token per request, history
 // [0, seq)): the same kernels without the fresh-token workgroup, and a
