@@ -177,19 +177,45 @@ constexpr size_t kPartialFloats = kPartO + 2 * kRows;
 
 // The item of split-kernel workgroup b (the split grid is one dimension of
 // exactly the launch's workgroups, item by item: each item's history splits,
-// then its fresh-token workgroup when it has one), and b's index within it.
-// Item i's workgroups start at pbase(i) - i * (fresh - fresh_block), a
-// non-decreasing sequence: the item is the last one whose start is <= b.
-__device__ __forceinline__ int locate_item(const DecodeArgs& a, int b, int& local) {
+// then its fresh-token workgroup when it has one), b's index within it, and
+// the item's fields.  Item i's workgroups start at pbase(i) - i * (fresh -
+// fresh_block), a non-decreasing sequence: the item is the last one whose
+// start is <= b, i.e. the number of starts <= b, less one.  Every lane reads
+// items `lane` and `lane + 64` (all inline items) in one round of independent
+// loads, a ballot counts the starts, and the chosen item's fields come from
+// its lane: one memory round trip, where a search would take a dependent
+// round trip per halving.  Called by every lane of the wavefront.
+static_assert(kMaxInlineItems <= 128, "two items per lane");
+__device__ __forceinline__ ItemInfo find_item(const DecodeArgs& a, int b, int& item, int& local) {
   const int skip = a.fresh - a.fresh_block;     // fresh slots without a workgroup of their own
-  int lo = 0, hi = a.nitems - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (a.items[mid].pbase - mid * skip <= b) lo = mid;
-    else hi = mid - 1;
+  const int lane = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  // (unconditional loads, lanes past the last item reading item 0, so that
+  // all ten go out before one wait)
+  const int n = a.nitems;
+  const int* f0 = reinterpret_cast<const int*>(&a.items[lane < n ? lane : 0]);
+  const int* f1 = reinterpret_cast<const int*>(&a.items[lane + 64 < n ? lane + 64 : 0]);
+  int w0[5], w1[5];
+#pragma unroll
+  for (int k = 0; k < 5; ++k) {
+    w0[k] = f0[k];
+    w1[k] = f1[k];
   }
-  local = b - (a.items[lo].pbase - lo * skip);
-  return lo;
+  static_assert(offsetof(ItemInfo, pbase) == 2 * sizeof(int), "pbase is the third word");
+  const int s0 = lane < n ? w0[2] - lane * skip : 0x7fffffff;
+  const int s1 = lane + 64 < n ? w1[2] - (lane + 64) * skip : 0x7fffffff;
+  item = __popcll(__ballot(s0 <= b)) + __popcll(__ballot(s1 <= b)) - 1;
+  item = __builtin_amdgcn_readfirstlane(item);
+  int fld[5];
+#pragma unroll
+  for (int k = 0; k < 5; ++k) {
+    const int v0 = __builtin_amdgcn_readlane(w0[k], item & 63), v1 = __builtin_amdgcn_readlane(w1[k], item & 63);
+    fld[k] = item < 64 ? v0 : v1;
+  }
+  static_assert(sizeof(ItemInfo) == 5 * sizeof(int), "ItemInfo is five words");
+  ItemInfo it;
+  __builtin_memcpy(&it, fld, sizeof(it));
+  local = b - (it.pbase - item * skip);
+  return it;
 }
 
 __device__ __forceinline__ int64_t partial_index(const DecodeArgs& a, const ItemInfo& it, int split, int rt) {
@@ -453,10 +479,9 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   // last steps hold the window tokens, whose extra passes make them the
   // longest workgroups, so they start first (measured: C5 decode 37.6 ->
   // 34 us, C2 unchanged).
-  int bx;
-  const int item = locate_item(a, (int)blockIdx.x, bx);
+  int bx, item;
+  const ItemInfo it = find_item(a, (int)blockIdx.x, item, bx);
   const int rt = blockIdx.z;
-  const ItemInfo it = a.items[item];
   const int rows = it.nq * a.group;
   if (it.nq <= 0 || rt * kRows >= rows) return;
   if (bx >= it.nsplit) {                  // the fresh-token workgroup, or none for this item
@@ -1101,9 +1126,8 @@ __device__ __forceinline__ float ror8_add(float x) {
 
 __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
-  int bx;
-  const int item = locate_item(a, (int)blockIdx.x, bx);
-  const ItemInfo it = a.items[item];
+  int bx, item;
+  const ItemInfo it = find_item(a, (int)blockIdx.x, item, bx);
   const int rows = it.nq * a.group;
   if (it.nq <= 0 || blockIdx.z != 0) return;
   if (bx >= it.nsplit) {                  // the fresh-token workgroup, or none for this item
