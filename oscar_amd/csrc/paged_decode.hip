@@ -1002,7 +1002,11 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
 // rows at the end.  A tile's bytes (K codes, meta, V codes, owner tags) are
 // copied straight into a 3-slot LDS ring of the wavefront by buffer loads to
 // LDS, two tiles ahead of the one being computed, so that the history
-// streams without holding registers for the loads in flight.
+// streams without holding registers for the loads in flight.  Window-owned
+// tokens are left out of a tile and added by a window pass from the fp16
+// images; a wavefront takes its last tile first (the recent window's, when
+// it holds any) and runs that tile's window pass at once, while the next two
+// tiles arrive, and the other window tiles' passes after its last tile.
 //
 // Lane l = (c, G), c = l % 16, G = l / 16, on v_mfma_f32_16x16x32_f16:
 //  * S^T = K Q^T for each half h of the tile: A = K (16 tokens x 32
@@ -1192,8 +1196,14 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(Decode
     return (p >= 0 && p < a.num_pages) ? p : -1;
   };
   auto tile_pos = [&](int k) { return (split + nsplit * k) * kStepTok + kTile * w; };
-  auto issue = [&](int k) {
-    load_small_tile(a, S.ring[w][k % kSmRing], tile_page(k), tile_pos(k), prefix, kvh, lane);
+  // Processing order: the wavefront's last tile first (the one that holds the
+  // recent window when any does, so its window pass can run while the next
+  // tiles are in flight), then tiles 0, 1, ...; ring slot i % kSmRing holds the
+  // i-th tile processed.
+  auto tile_of = [&](int i) { return nst > 1 ? (i == 0 ? nst - 1 : i - 1) : i; };
+  auto issue = [&](int i) {
+    const int k = tile_of(i);
+    load_small_tile(a, S.ring[w][i % kSmRing], tile_page(k), tile_pos(k), prefix, kvh, lane);
   };
 
   // ---- Q^T operands (column c: high part of row c, or low part of row c - 8)
@@ -1257,12 +1267,13 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(Decode
 
   // One tile of INT2 tokens.  Window-owned tokens (bits of wm) are left out
   // here (score -inf, no weight) and added by the window pass after the loop.
-  auto tile_body = [&](const SmallSlot& L, int k, int nvalid, uint32_t wm) {
-    // Tile k + 2 goes into the slot tile k - 1 left (its LDS reads are complete: lgkmcnt(0)).
-    if (k + 2 < nst) {
+  auto tile_body = [&](const SmallSlot& L, int i, int nvalid, uint32_t wm) {
+    // The tile processed i + 2-th goes into the slot the one before this left
+    // (its LDS reads are complete: lgkmcnt(0)).
+    if (i + 2 < nst) {
       __builtin_amdgcn_s_waitcnt(0xC07F);
       asm volatile("" ::: "memory");
-      issue(k + 2);
+      issue(i + 2);
     }
     // ---- token parameters (lane t32 < 32) and the byte-transposed V codes ----
     bool big;
@@ -1381,33 +1392,10 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(Decode
     return (uint32_t)__ballot(st);
   };
 
-  uint64_t wtiles = 0;             // tiles k of this wavefront that hold window tokens
-#pragma unroll 1
-  for (int k = 0; k < nst; ++k) {
-    // Wait for tile k's loads, leaving tile k + 1's in flight (tile k + 2 is
-    // requested in the tile body).
-    if (k + 1 < nst)
-      wait_vmcnt<kSmallLoadsPerTile>();
-    else
-      wait_vmcnt<0>();
-    asm volatile("" ::: "memory");
-    const SmallSlot& L = S.ring[w][k % kSmRing];
-    const int page = tile_page(k);
-    const int nvalid = page >= 0 ? min(kTile, max(prefix - tile_pos(k), 0)) : 0;
-    const uint32_t wm = window_bits(k, (int)L.own[t32][0]);
-    if (wm != 0u) {
-      wtiles |= 1ull << k;
-      S.wbits[w][k] = wm;
-    }
-    tile_body(L, k, nvalid, wm);
-  }
-
-  // ---- the window tokens: K from the fp16 image (high and low parts), V
-  // from the V image, probabilities p / 4 into the same accumulators ----
-#pragma unroll 1
-  while (wtiles != 0ull) {
-    const int k = __builtin_ctzll(wtiles);
-    wtiles &= wtiles - 1;
+  // The window tokens of tile k: K from the fp16 image (high and low parts),
+  // V from the V image (high and low parts), probabilities p / 4 into the
+  // same accumulators.
+  auto window_tile = [&](int k) {
     const int page = tile_page(k);
     const int prow0 = (int)fast_mod((uint32_t)tile_pos(k), a.bs_div);
     const uint32_t wm = __builtin_amdgcn_readfirstlane(S.wbits[w][k]);
@@ -1478,6 +1466,49 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(Decode
     for (int n = 0; n < 16; ++n) acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv[n], pwop, acc[n], 0, 0, 0);
 #pragma unroll
     for (int n = 0; n < 16; ++n) acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl[n], pwop, acc[n], 0, 0, 0);
+    };
+
+  uint64_t wtiles = 0;             // tiles k of this wavefront that hold window tokens
+  // One tile: wait for its loads, leaving the next one's in flight (the one
+  // after is requested in the tile body); returns its window bits.
+  auto step_tile = [&](int i) -> uint32_t {
+    if (i + 1 < nst)
+      wait_vmcnt<kSmallLoadsPerTile>();
+    else
+      wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    const SmallSlot& L = S.ring[w][i % kSmRing];
+    const int k = tile_of(i);
+    const int page = tile_page(k);
+    const int nvalid = page >= 0 ? min(kTile, max(prefix - tile_pos(k), 0)) : 0;
+    const uint32_t wm = window_bits(k, (int)L.own[t32][0]);
+    if (wm != 0u) {
+      wtiles |= 1ull << k;
+      S.wbits[w][k] = wm;
+    }
+    tile_body(L, i, nvalid, wm);
+    return wm;
+  };
+  int i0 = 0;
+  if (nst > 1) {
+    // The first tile processed (the wavefront's last) and, at once, its
+    // window tokens, while the next two tiles arrive; peeled off the loop so
+    // that the window pass's registers stay out of it.
+    if (step_tile(0) != 0u) {
+      wtiles &= ~(1ull << (nst - 1));
+      window_tile(nst - 1);
+    }
+    i0 = 1;
+  }
+#pragma unroll 1
+  for (int i = i0; i < nst; ++i) step_tile(i);
+
+  // ---- the window tiles not done yet ----
+#pragma unroll 1
+  while (wtiles != 0ull) {
+    const int k = __builtin_ctzll(wtiles);
+    wtiles &= wtiles - 1;
+    window_tile(k);
   }
 
   // ---- the four wavefronts' rows combined into the split's partial ----
