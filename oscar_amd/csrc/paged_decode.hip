@@ -65,10 +65,12 @@
 // DecodeOnly read (no fresh K/V; one query token per request, history
 // [0, seq)): the same kernels without the fresh-token workgroup, and a
 // staged value replaces the INT2 one only at positions p < head or p >= cut
-// of the request.  A bounds kernel computes (head, cut) on the device first:
-// head is the sink length when every seat of the sink pages holds its page,
-// else 0; cut starts the run of staged positions that ends at seq - 1 inside
-// [max(seq - recent, head), seq).
+// of the request: head is the sink length when every seat of the sink pages
+// holds its page, else 0; cut starts the run of staged positions that ends
+// at seq - 1 inside [max(seq - recent, head), seq).  The small-row kernel's
+// kFold instance finds (head, cut) in its prologue (at most 256 sink and
+// recent positions: one of each per thread); other launches run a bounds
+// kernel first.
 #include <type_traits>
 
 #include "oscar_common.h"
@@ -136,6 +138,8 @@ struct DecodeArgs {
   int32_t max_splits, row_tiles;  // the largest nsplit of the launch; row tiles per item
   int32_t nitems;               // items of the launch chunk
   ItemInfo items[kMaxInlineItems];
+  int32_t win_fold;             // DecodeOnly through the small-row kernel: it finds (head, cut) itself
+  int32_t win_sink, win_recent; // ... from sink_eff and recent (each at most 256: one position per thread)
 };
 
 // One step is 128 history tokens, one 32-token tile per wavefront.  Only the
@@ -1045,6 +1049,7 @@ struct SmallLds {
   SmallTileLds tile[kWaves];
   uint32_t wbits[kWaves][kMaxTilesPerSplit / kWaves];   // window-token bits of each of the wavefront's tiles
   SmallSlot ring[kWaves][kSmRing];
+  int32_t wbound[kWaves][2];     // folded DecodeOnly bounds: a sink position not staged, highest recent one
 };
 
 struct SmallCombineLds {
@@ -1128,6 +1133,9 @@ __device__ __forceinline__ float ror8_add(float x) {
   return x + dpp_move<0x128>(x);          // row_ror:8: lane c takes lane (c + 8) % 16 of its row
 }
 
+// kFold: the DecodeOnly read whose window bounds the kernel finds itself
+// (a.win_fold); the other instance runs every other small-row launch.
+template <bool kFold>
 __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
   int bx, item;
@@ -1201,9 +1209,47 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(Decode
   // tiles are in flight), then tiles 0, 1, ...; ring slot i % kSmRing holds the
   // i-th tile processed.
   auto tile_of = [&](int i) { return nst > 1 ? (i == 0 ? nst - 1 : i - 1) : i; };
+  // Folded DecodeOnly bounds (the bounds kernel's rule, one sink and one
+  // recent position per thread): the owner tags are requested here, before
+  // the tiles, and compared after the tile requests, so their round trip
+  // overlaps the Q^T set-up and the first tiles' flight.
+  const bool fold = kFold;
+  const bool sink_len = fold && a.win_sink > 0 && prefix > a.win_sink;
+  const int rlo = max(prefix - a.win_recent, 0);
+  const int ps = tid, pr = prefix - 1 - tid;
+  bool chk_s = false, chk_r = false;
+  int pg_s = -1, pg_r = -1;
+  int64_t own_s = -1, own_r = -1;
+  uint32_t pis = 0, pir = 0;
+  if (fold) {
+    const int32_t* bt_row = a.block_table + (int64_t)it.req * a.bt_stride;
+    chk_s = sink_len && ps < a.win_sink;
+    chk_r = pr >= rlo;
+    pis = fast_div((uint32_t)(chk_s ? ps : 0), a.bs_div);
+    pir = fast_div((uint32_t)(chk_r ? pr : 0), a.bs_div);
+    if (chk_s && (int)pis < a.bt_cols) pg_s = bt_row[pis];
+    if (chk_r && (int)pir < a.bt_cols) pg_r = bt_row[pir];
+  }
+  // The pages of the first two tiles, read (after the page loads above) into
+  // scalar registers before the owner tags are requested, so that the tile
+  // requests below never wait for those.
+  int page_i0 = -1, page_i1 = -1;
+  if (fold) {
+    page_i0 = tile_page(tile_of(0));
+    page_i1 = nst > 1 ? tile_page(tile_of(1)) : -1;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (fold) {
+    auto seat = [&](int page, int pos, uint32_t pi) {
+      return (int64_t)fast_mod((uint32_t)page, a.rows_div) * a.block_size + (pos - (int)pi * a.block_size);
+    };
+    if (pg_s >= 0 && pg_s < a.num_pages) own_s = a.owner[seat(pg_s, ps, pis)];
+    if (pg_r >= 0 && pg_r < a.num_pages) own_r = a.owner[seat(pg_r, pr, pir)];
+  }
   auto issue = [&](int i) {
     const int k = tile_of(i);
-    load_small_tile(a, S.ring[w][i % kSmRing], tile_page(k), tile_pos(k), prefix, kvh, lane);
+    const int page = (fold && i < 2) ? (i == 0 ? page_i0 : page_i1) : tile_page(k);
+    load_small_tile(a, S.ring[w][i % kSmRing], page, tile_pos(k), prefix, kvh, lane);
   };
 
   // ---- Q^T operands (column c: high part of row c, or low part of row c - 8)
@@ -1232,8 +1278,32 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(Decode
   // the first two tiles (the page reads above are complete by now)
   issue(0);
   if (nst > 1) issue(1);
+  if (fold) {
+    // a position checked is staged when its page is in range and owns the seat
+    const bool bad_s = chk_s && !(pg_s >= 0 && pg_s < a.num_pages && own_s == (int64_t)pg_s);
+    const bool bad_r = chk_r && !(pg_r >= 0 && pg_r < a.num_pages && own_r == (int64_t)pg_r);
+    int h = bad_r ? pr : -1;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) h = max(h, __shfl_xor(h, o, 64));
+    const bool any_s = __ballot(bad_s) != 0ull;
+    if (lane == 0) {
+      S.wbound[w][0] = any_s ? 1 : 0;
+      S.wbound[w][1] = h;
+    }
+  }
   lds_barrier();
   const float qsum = (S.qs[0][r] + S.qs[1][r]) + (S.qs[2][r] + S.qs[3][r]);
+  if (fold) {
+    int sb = 0, hb = -1;
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k) {
+      sb |= S.wbound[k][0];
+      hb = max(hb, S.wbound[k][1]);
+    }
+    win_head = (sink_len && sb == 0) ? a.win_sink : 0;
+    const int t0 = max(prefix - a.win_recent, win_head);
+    win_tail = hb >= t0 ? hb + 1 : t0;
+  }
 
   floatx4 acc[16];                 // O^T tile n = 4q + 2mh + b
 #pragma unroll
@@ -2072,14 +2142,15 @@ int fill_common(DecodeArgs& a, const float* q_rot, int32_t num_heads, int32_t nu
   return kOk;
 }
 
-std::atomic<uint64_t> g_split_lds_set[3] = {{0}, {0}, {0}};
+std::atomic<uint64_t> g_split_lds_set[4] = {{0}, {0}, {0}, {0}};
 
 int set_split_lds() {
-  const void* k[3] = {reinterpret_cast<const void*>(paged_decode_split_kernel<false>),
+  const void* k[4] = {reinterpret_cast<const void*>(paged_decode_split_kernel<false>),
                       reinterpret_cast<const void*>(paged_decode_split_kernel<true>),
-                      reinterpret_cast<const void*>(paged_decode_split_small_kernel)};
-  const size_t bytes[3] = {kLdsBytes, kLdsBytes, kSmallLdsBytes};
-  for (int i = 0; i < 3; ++i) {
+                      reinterpret_cast<const void*>(paged_decode_split_small_kernel<false>),
+                      reinterpret_cast<const void*>(paged_decode_split_small_kernel<true>)};
+  const size_t bytes[4] = {kLdsBytes, kLdsBytes, kSmallLdsBytes, kSmallLdsBytes};
+  for (int i = 0; i < 4; ++i) {
     const int rc = set_dynamic_lds(k[i], (int)bytes[i], g_split_lds_set[i]);
     if (rc != kOk) return rc;
   }
@@ -2107,9 +2178,14 @@ void launch_split(const DecodeArgs& a, unsigned nitems, dim3 grid, hipStream_t s
     const int64_t r = (int64_t)a.items[i].nq * a.group;
     max_rows = r > max_rows ? r : max_rows;
   }
-  if (max_rows <= kSmRows)
-    hipLaunchKernelGGL(paged_decode_split_small_kernel, grid, dim3(256), kSmallLdsBytes, stream, a);
-  else if (multi)
+  // (a folded DecodeOnly launch has at most 8 rows per item: oscar_decode_only
+  // folds only then)
+  if (max_rows <= kSmRows) {
+    if (a.win_fold)
+      hipLaunchKernelGGL(paged_decode_split_small_kernel<true>, grid, dim3(256), kSmallLdsBytes, stream, a);
+    else
+      hipLaunchKernelGGL(paged_decode_split_small_kernel<false>, grid, dim3(256), kSmallLdsBytes, stream, a);
+  } else if (multi)
     hipLaunchKernelGGL((paged_decode_split_kernel<true>), grid, dim3(256), kLdsBytes, stream, a);
   else
     hipLaunchKernelGGL((paged_decode_split_kernel<false>), grid, dim3(256), kLdsBytes, stream, a);
@@ -2457,7 +2533,14 @@ int oscar_decode_only(const float* q_rot, int32_t num_heads, int32_t num_kv_head
   const int32_t sink_eff = window ? (sink_tokens / block_size) * block_size : 0;
   a.k_new = nullptr;
   a.v_new = nullptr;
-  a.win = window ? bounds : nullptr;
+  // One query per request: the small-row kernel reads when the group has at
+  // most 8 heads, and then finds the bounds itself when each of the sink and
+  // recent spans fits one position per thread; else the bounds kernel runs.
+  const bool fold = window && a.group <= kSmRows && sink_eff <= 256 && recent_tokens <= 256;
+  a.win = window && !fold ? bounds : nullptr;
+  a.win_fold = fold ? 1 : 0;
+  a.win_sink = sink_eff;
+  a.win_recent = recent_tokens;
   a.fresh = 0;
   a.row_tiles = (a.group + kRows - 1) / kRows;
   if ((rc = set_split_lds()) != kOk) return rc;
@@ -2469,7 +2552,7 @@ int oscar_decode_only(const float* q_rot, int32_t num_heads, int32_t num_kv_head
     a.block_table = block_table ? block_table + (int64_t)c0 * block_table_stride : nullptr;
     const unsigned nitems = (unsigned)(nreq * num_kv_heads);
     if (!plan_splits(a, nitems, max_history, tiles_per_split, 0)) return kErrInvalidArgument;
-    if (window) {
+    if (window && !fold) {
       hipLaunchKernelGGL(decode_only_bounds_kernel, dim3((unsigned)nreq), dim3(kBoundsThreads), 0, stream, a, bounds,
                          sink_eff, recent_tokens);
       if (hipGetLastError() != hipSuccess) return kErrLaunch;

@@ -58,6 +58,18 @@ def test_mixed_requests_planted_gaps(device, hk, hq):
     run_case(case, device, plant=[(0, 1), (2, case.seqs[2] - 5), (5, case.seqs[5] - 1)])
 
 
+@pytest.mark.parametrize("hq,sink,recent", [(6, 256, 256), (16, 64, 64), (6, 64, 320), (6, 288, 64)])
+def test_planted_gaps_on_both_bounds_paths(device, hq, sink, recent):
+    """The small-row split kernel finds the window bounds itself when the
+    group has at most 8 heads and the sink and recent spans are at most 256
+    positions (the first case, at that limit); more heads per group (the
+    cooperative kernel) or a longer span keep the separate bounds kernel."""
+    hist = [300, 5, 1000, 129, 63, 2047]
+    case = decode_case(hist, [1] * len(hist), bs=32, seed=48, sink=sink, recent=recent, staging=4096, hk=1, hq=hq,
+                       pool_pages=sum((h + 32) // 32 for h in hist) + 5)
+    run_case(case, device, plant=[(0, 1), (2, case.seqs[2] - 5), (5, case.seqs[5] - 1), (5, case.seqs[5] - 200)])
+
+
 @pytest.mark.parametrize("bs", [64, 128])
 def test_default_window_long_histories(device, bs):
     hist = [5000, 333, 4097, 24, 128]
