@@ -1345,6 +1345,10 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(Decode
       asm volatile("" ::: "memory");
       issue(i + 2);
     }
+    // A tile without INT2 tokens (every valid token window-owned, or none
+    // valid) adds nothing here: all its scores would be masked out.
+    const uint32_t valid = nvalid >= kTile ? ~0u : ((1u << nvalid) - 1u);
+    if ((valid & ~wm) == 0u) return;
     // ---- token parameters (lane t32 < 32) and the byte-transposed V codes ----
     bool big;
     {
