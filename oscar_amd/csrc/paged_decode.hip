@@ -243,6 +243,9 @@ __device__ __forceinline__ uint32_t magic_pair(uint32_t w, int sh, uint32_t ones
 
 __device__ __forceinline__ float exp2_raw(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Bits of a tile's valid tokens (the first n of its 32).
+__device__ __forceinline__ uint32_t tile_valid(int n) { return n >= 32 ? ~0u : (n <= 0 ? 0u : (1u << n) - 1u); }
+
 __device__ __forceinline__ half8 as_half8(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3) {
   return __builtin_bit_cast(half8, u32x4{d0, d1, d2, d3});
 }
@@ -732,13 +735,20 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
       } else {
         const bool wl = (wmw >> col) & 1u;
         const u32x4* img_lo = img + 16 * 64;
+        // a tile whose valid tokens are all window-owned needs no code operands
+        const bool all_win = (tile_valid(nvalid) & ~wmw) == 0u;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           half8 ka[2];
-          k_operands(kw[j], ones16, ka);
+          if (all_win) {
+            ka[0] = __builtin_bit_cast(half8, im[2 * j]);
+            ka[1] = __builtin_bit_cast(half8, im[2 * j + 1]);
+          } else {
+            k_operands(kw[j], ones16, ka);
 #pragma unroll
-          for (int aa = 0; aa < 2; ++aa)
-            ka[aa] = wl ? __builtin_bit_cast(half8, im[2 * j + aa]) : ka[aa];
+            for (int aa = 0; aa < 2; ++aa)
+              ka[aa] = wl ? __builtin_bit_cast(half8, im[2 * j + aa]) : ka[aa];
+          }
           qk_pair(j, ka[0], ka[1]);
           // As soon as a k-step pair of the high part is used, its registers
           // take the same pair of the low part, zero for lanes of tokens
@@ -871,20 +881,24 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
 #pragma unroll
     for (int j = 0; j < kWaves; ++j) {
       if (pgs[j] < 0 || tbase + kTile * j >= prefix) continue;
-      const uint32_t* vr = &B.vt[j][vrow * kVtRow];
-      const _Float16* pr = &S.p[j][col * kPRow + 8 * g];
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const uint32_t d0 = vr[4 * s2 + 2 * g], d1 = vr[4 * s2 + 2 * g + 1];
-        const half8 pop = *reinterpret_cast<const half8*>(pr + 16 * s2);
-        const half8 v0 = as_half8(pair_lo(d0, ls0, ones16), pair_hi(d0, rs0, ones16), pair_lo(d1, ls0, ones16),
-                                  pair_hi(d1, rs0, ones16));
-        const half8 v1 = as_half8(pair_lo(d0, ls1, ones16), pair_hi(d0, rs1, ones16), pair_lo(d1, ls1, ones16),
-                                  pair_hi(d1, rs1, ones16));
-        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v0, pop, acc[0], 0, 0, 0);
-        acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v1, pop, acc[1], 0, 0, 0);
-      }
       const uint32_t wmj = j == 0 ? wm0 : (j == 1 ? wm1 : (j == 2 ? wm2 : wm3));
+      // a tile without INT2 tokens has all its P' zero: only its window part
+      const bool int2 = (tile_valid(min(kTile, prefix - (tbase + kTile * j))) & ~wmj) != 0u;
+      if (int2) {
+        const uint32_t* vr = &B.vt[j][vrow * kVtRow];
+        const _Float16* pr = &S.p[j][col * kPRow + 8 * g];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const uint32_t d0 = vr[4 * s2 + 2 * g], d1 = vr[4 * s2 + 2 * g + 1];
+          const half8 pop = *reinterpret_cast<const half8*>(pr + 16 * s2);
+          const half8 v0 = as_half8(pair_lo(d0, ls0, ones16), pair_hi(d0, rs0, ones16), pair_lo(d1, ls0, ones16),
+                                    pair_hi(d1, rs0, ones16));
+          const half8 v1 = as_half8(pair_lo(d0, ls1, ones16), pair_hi(d0, rs1, ones16), pair_lo(d1, ls1, ones16),
+                                    pair_hi(d1, rs1, ones16));
+          acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v0, pop, acc[0], 0, 0, 0);
+          acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v1, pop, acc[1], 0, 0, 0);
+        }
+      }
       if (wmj != 0u) {
         const _Float16* pwr = &S.pw[j][col * kPRow + 8 * g];
 #pragma unroll
@@ -1347,8 +1361,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(Decode
     }
     // A tile without INT2 tokens (every valid token window-owned, or none
     // valid) adds nothing here: all its scores would be masked out.
-    const uint32_t valid = nvalid >= kTile ? ~0u : ((1u << nvalid) - 1u);
-    if ((valid & ~wm) == 0u) return;
+    if ((tile_valid(nvalid) & ~wm) == 0u) return;
     // ---- token parameters (lane t32 < 32) and the byte-transposed V codes ----
     bool big;
     {
