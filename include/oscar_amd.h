@@ -47,6 +47,22 @@ size_t oscar_rotation_operand_bytes(int32_t head_size);
 int oscar_rotation_operand(const float* rotation, void* operand, int32_t head_size,
                            oscar_stream_t stream);
 
+/* Rows rotated on MFMA: out[r] = in[r] @ R for rows of head_size features.
+ * Replaces the prefill route's fp32 rotations (oscar_ascend/backend.py:392-413:
+ * q / k / v `x.float() @ rk` / `@ rv` before the attention, `out.float() @
+ * rv.t()` after it).
+ *   in:          [rows][in_row_stride] bf16 (in_f32 = 0) or fp32 (in_f32 = 1);
+ *   rot_operand: oscar_rotation_operand of R (of R_v^T for the output);
+ *   out:         [rows][out_row_stride] fp32 (out_bf16 = 0) or bf16 (out_bf16 = 1,
+ *                rounded to nearest even).
+ * fp32 input enters as bf16 high + low parts, R as the operand's parts, with
+ * fp32 accumulation: about 2^-16 of each product.  Row starts must be 16-byte
+ * aligned.
+ */
+int oscar_rotate_rows(const void* in, int32_t in_f32, int64_t in_row_stride, int64_t rows, int32_t head_size,
+                      const void* rot_operand, void* out, int32_t out_bf16, int64_t out_row_stride,
+                      oscar_stream_t stream);
+
 /* ---------------------------------------------------------------- quantize-write
  * Fused rotate + clip + INT2 quantize + pack + paged-slot write.
  * Replaces do_kv_cache_update's _rotate_clip + oscar_store_triton

@@ -166,6 +166,8 @@ class OscarAttentionBackendImpl:
             layer._oscar_rkT = rk.t().contiguous()
             layer._oscar_rvT = rv.t().contiguous()
             layer._oscar_rot_ops = (rk, rv, quant.rotation_operand(rk), quant.rotation_operand(rv))
+            # the output rotation of the prefill route (out @ R_v^T) on MFMA
+            layer._oscar_rvT_op = quant.rotation_operand(layer._oscar_rvT)
         return layer._oscar_rots
 
     # ------------------------------------------------------------------ write path
@@ -424,12 +426,24 @@ class OscarAttentionBackendImpl:
                 attn_out[sl] = res
             else:
                 attn_out[idx] = res
+        # bf16 models rotate on MFMA (oscar_rotate_rows: about 2^-16 of each
+        # product, below the fp16 rounding the prefill kernel's operands take
+        # and the bf16 output's); other dtypes keep the fp32 matmuls.
+        mfma_rot = query.dtype == key.dtype == value.dtype == torch.bfloat16
+        _, _, op_k, op_v = layer._oscar_rot_ops
         for i, a, b, seq in large:
             cached = seq - (b - a)
-            out_rot = prefill.prefill_continuation(
-                q3[a:b].float() @ rk, k3[a:b].float() @ rk, v3[a:b].float() @ rv,
-                self.key_cache, self.value_cache, bt[i], max(cached, 0), self.scale, stage)
-            attn_out[a:b] = (out_rot @ rvT).to(query.dtype)
+            if mfma_rot:
+                qr, kr, vr = (quant.rotate_rows(q3[a:b], op_k), quant.rotate_rows(k3[a:b], op_k),
+                              quant.rotate_rows(v3[a:b], op_v))
+            else:
+                qr, kr, vr = q3[a:b].float() @ rk, k3[a:b].float() @ rk, v3[a:b].float() @ rv
+            out_rot = prefill.prefill_continuation(qr, kr, vr, self.key_cache, self.value_cache, bt[i],
+                                                   max(cached, 0), self.scale, stage)
+            if mfma_rot:
+                quant.rotate_rows(out_rot, layer._oscar_rvT_op, torch.bfloat16, out=attn_out[a:b])
+            else:
+                attn_out[a:b] = (out_rot @ rvT).to(query.dtype)
         return attn_out
 
 

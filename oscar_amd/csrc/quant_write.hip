@@ -475,6 +475,10 @@ __global__ __launch_bounds__(256, 2) void quant_write_fused_kernel(
     else wait_vmcnt<0>();
     lds_barrier();
     if (m + 3 < kSteps) request(m + 3);
+    // The waits of steps 5-7 count x_8..15 after chunk 7's copies: keep the
+    // scheduler from hoisting any of those loads above the request (one
+    // hoisted load would leave chunk 7's last copy unwaited at step 7).
+    __builtin_amdgcn_sched_barrier(0);
     if (m == 4) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) xhi[k] = load_x(8 + k);
@@ -517,6 +521,153 @@ __global__ __launch_bounds__(256, 2) void quant_write_fused_kernel(
   if (w.rows > 0 && slot >= 0) window_epilogue(v, tok, slot, head, side, half, c.block_size, w);
 }
 
+// ---------------------------------------------------------------------------
+// Rows rotated on MFMA: out = in @ R for rows of D = 256 features (the
+// prefill route's q / k / v rotations and its output's R_v^T,
+// oscar_ascend/backend.py:392-413).  in: bf16 (an exact operand) or fp32
+// (its bf16 high and low parts); R: the operand's bf16 high and low parts;
+// fp32 accumulation (about 2^-16 of each product); out: fp32, or bf16
+// rounded to nearest even.
+// grid = ceil(rows / 128), block = 256 (4 waves x 32 rows): lane l takes row
+// (l & 31) of its wave, input and output features 128 (l >> 5) .. +127, and
+// the operand streams through the fused kernel's 4-slot LDS ring.  A bf16
+// input's first half (K steps 0-7) is requested before the ring and its
+// second half during step 4; an fp32 input (twice the registers) comes in
+// quarters, the first before the ring and quarter q (steps 4q .. 4q + 3)
+// during step 4q - 3.  kRotWait gives each step's wait: the loads issued
+// after the last one the step needs (its chunk and its input).
+// ---------------------------------------------------------------------------
+template <bool kF32In>
+struct RotSched {
+  static constexpr int kParts = kF32In ? 4 : 2;                 // input parts (quarters / halves)
+  static constexpr int kPartLoads = 2 * kSteps / kParts / (kF32In ? 1 : 2);   // 16-byte loads per part
+  // step during which part p (> 0) is requested
+  static __device__ constexpr int step_of(int p) { return kF32In ? 4 * p - 3 : 4; }
+};
+template <bool kF32In>
+__device__ constexpr int kRotWait(int m) {
+  return kF32In ? (m == 14 ? 4 : m == 15 ? 0 : ((m & 3) >= 2 ? 16 : 8))
+                : ((m >= 5 && m <= 7) ? 16 : m == 14 ? 4 : m == 15 ? 0 : 8);
+}
+
+template <bool kF32In, bool kBf16Out>
+__global__ __launch_bounds__(256, 2) void rotate_rows_kernel(const void* __restrict__ in, int64_t in_stride,
+                                                            int64_t rows, const uint8_t* __restrict__ rop,
+                                                            void* __restrict__ out, int64_t out_stride) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
+  using Sched = RotSched<kF32In>;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int half = lane >> 5;
+  const int64_t row = (int64_t)blockIdx.x * (kFusedWaves * kTokPerWave) + wave * kTokPerWave + (lane & 31);
+  const bool live = row < rows;
+  const int64_t rr = live ? row : 0;        // a lane past the last row computes row 0 and stores nothing
+  // input of K step m: features 128 half + 8m .. +7 (one 16-byte load, or two for fp32)
+  u32x4 xr[Sched::kParts * Sched::kPartLoads];
+  const uint8_t* xsrc = static_cast<const uint8_t*>(in) + (rr * in_stride + kPerLane * half) * (kF32In ? 4 : 2);
+  auto load_part = [&](int p) {
+#pragma unroll
+    for (int i = 0; i < Sched::kPartLoads; ++i)
+      xr[p * Sched::kPartLoads + i] = reinterpret_cast<const u32x4*>(xsrc)[p * Sched::kPartLoads + i];
+  };
+  load_part(0);
+  typedef __attribute__((address_space(3))) void lds_void;
+  const __amdgpu_buffer_rsrc_t rop_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)rop, (short)0, (int)(kSteps * kChunkBytes), 0x00020000);
+  auto request = [&](int chunk) {
+#pragma unroll
+    for (int i = 0; i < kDmaPerChunk; ++i) {
+      const int blk = kDmaPerChunk * wave + i;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rop_rsrc, (lds_void*)(uintptr_t)(uint32_t)(uintptr_t)(ring + (chunk % kRing) * kChunkBytes + blk * 1024),
+          16, chunk * kChunkBytes + (blk * 64 + lane) * 16, 0, 0, 0);
+    }
+  };
+  request(0);
+  request(1);
+  request(2);
+  floatx16 acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc[t] = floatx16{};
+  constexpr int kPairs = kF32In ? 24 : 16;      // (fragment, operand) products per K step
+#pragma unroll
+  for (int m = 0; m < kSteps; ++m) {
+    {
+      // (m is a constant once the loop is unrolled: one wait remains)
+      const int wn = kRotWait<kF32In>(m);
+      if (wn == 24) wait_vmcnt<24>();
+      else if (wn == 16) wait_vmcnt<16>();
+      else if (wn == 8) wait_vmcnt<8>();
+      else if (wn == 4) wait_vmcnt<4>();
+      else wait_vmcnt<0>();
+    }
+    lds_barrier();
+    if (m + 3 < kSteps) request(m + 3);
+    // the wait counts above assume every input load of a part after this
+    // step's chunk request: keep the scheduler from hoisting one
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 1; p < Sched::kParts; ++p)
+      if (m == Sched::step_of(p)) load_part(p);
+    bf16x8 xh, xl;
+    if constexpr (kF32In) {
+      const floatx4 f0 = __builtin_bit_cast(floatx4, xr[2 * m]), f1 = __builtin_bit_cast(floatx4, xr[2 * m + 1]);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float v = u < 4 ? f0[u] : f1[u - 4];
+        const __bf16 h = (__bf16)v;
+        xh[u] = h;
+        xl[u] = (__bf16)(v - (float)h);
+      }
+    } else {
+      xh = __builtin_bit_cast(bf16x8, xr[m]);
+      xl = xh;
+    }
+    // pair i < 16: fragment i (8 p + t) times the high part; i >= 16 (fp32
+    // input): fragment i - 16 (R's high part) times the low part
+    const u32x4* a_src = reinterpret_cast<const u32x4*>(ring + (m % kRing) * kChunkBytes);
+    constexpr int kAhead = 6;
+    bf16x8 a[kAhead];
+#pragma unroll
+    for (int i = 0; i < kAhead; ++i) a[i] = __builtin_bit_cast(bf16x8, a_src[(i & 15) * 64 + lane]);
+#pragma unroll
+    for (int i = 0; i < kPairs; ++i) {
+      const bf16x8 cur = a[i % kAhead];
+      if (i + kAhead < kPairs)
+        a[i % kAhead] = __builtin_bit_cast(bf16x8, a_src[((i + kAhead) & 15) * 64 + lane]);
+      acc[i & 7] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur, i < 16 ? xh : xl, acc[i & 7], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, kAhead, 0);
+#pragma unroll
+    for (int i = 0; i < kPairs; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i + kAhead < kPairs) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+  }
+  if (!live) return;
+  // register i of tile t: output feature 128 half + 16 t + i
+  if constexpr (kBf16Out) {
+    __bf16* dst = static_cast<__bf16*>(out) + row * out_stride + kPerLane * half;
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        bf16x8 o;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) o[u] = (__bf16)acc[t][8 * q + u];
+        *reinterpret_cast<bf16x8*>(dst + 16 * t + 8 * q) = o;
+      }
+  } else {
+    float* dst = static_cast<float*>(out) + row * out_stride + kPerLane * half;
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<floatx4*>(dst + 16 * t + 4 * q) =
+            floatx4{acc[t][4 * q], acc[t][4 * q + 1], acc[t][4 * q + 2], acc[t][4 * q + 3]};
+  }
+}
+
 // One thread per operand element (2 x 16 x 8 x 64 x 8 = 131072 entries), then
 // one per element of the fp32 copy of R that follows them (65536 entries).
 __global__ void rotation_operand_kernel(const float* __restrict__ R, __bf16* __restrict__ out) {
@@ -554,6 +705,7 @@ int check_cache_args(CacheArgs& c) {
 }
 
 std::atomic<uint64_t> g_lds_set{0};   // dynamic-LDS attribute set, one bit per device
+std::atomic<uint64_t> g_rot_lds_set[4] = {{0}, {0}, {0}, {0}};   // the same for the rotate_rows instances
 
 }  // namespace
 }  // namespace oscar
@@ -573,6 +725,45 @@ int oscar_rotation_operand(const float* rotation, void* operand, int32_t head_si
   const int total = kMfmaEntries + kHeadDim * kHeadDim;
   hipLaunchKernelGGL(rotation_operand_kernel, dim3((total + 255) / 256), dim3(256), 0, stream,
                      rotation, static_cast<__bf16*>(operand));
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+int oscar_rotate_rows(const void* in, int32_t in_f32, int64_t in_row_stride, int64_t rows, int32_t head_size,
+                      const void* rot_operand, void* out, int32_t out_bf16, int64_t out_row_stride,
+                      hipStream_t stream) {
+  if (head_size != kHeadDim) return kErrUnsupportedHeadDim;
+  if (rows < 0 || (in_f32 != 0 && in_f32 != 1) || (out_bf16 != 0 && out_bf16 != 1)) return kErrInvalidArgument;
+  if (rows == 0) return kOk;
+  if (!in || !rot_operand || !out || in_row_stride < kHeadDim || out_row_stride < kHeadDim)
+    return kErrInvalidArgument;
+  // 16-byte vector accesses: every row start 16-byte aligned
+  const int64_t in_bytes = in_f32 ? 4 : 2, out_bytes = out_bf16 ? 2 : 4;
+  if (((in_row_stride * in_bytes) & 15) || ((out_row_stride * out_bytes) & 15) ||
+      (reinterpret_cast<uintptr_t>(in) & 15) || (reinterpret_cast<uintptr_t>(out) & 15) ||
+      (reinterpret_cast<uintptr_t>(rot_operand) & 15))
+    return kErrInvalidArgument;
+  const int64_t per_block = kFusedWaves * kTokPerWave;
+  const dim3 grid((unsigned)((rows + per_block - 1) / per_block));
+  const uint8_t* rop = static_cast<const uint8_t*>(rot_operand);
+  const void* k[4] = {reinterpret_cast<const void*>(rotate_rows_kernel<false, false>),
+                      reinterpret_cast<const void*>(rotate_rows_kernel<false, true>),
+                      reinterpret_cast<const void*>(rotate_rows_kernel<true, false>),
+                      reinterpret_cast<const void*>(rotate_rows_kernel<true, true>)};
+  const int which = 2 * in_f32 + out_bf16;
+  constexpr int kRingLds = kRing * kChunkBytes;
+  if (set_dynamic_lds(k[which], kRingLds, g_rot_lds_set[which]) != kOk) return kErrLaunch;
+  if (in_f32 && out_bf16)
+    hipLaunchKernelGGL((rotate_rows_kernel<true, true>), grid, dim3(256), kRingLds, stream, in, in_row_stride, rows,
+                       rop, out, out_row_stride);
+  else if (in_f32)
+    hipLaunchKernelGGL((rotate_rows_kernel<true, false>), grid, dim3(256), kRingLds, stream, in, in_row_stride, rows,
+                       rop, out, out_row_stride);
+  else if (out_bf16)
+    hipLaunchKernelGGL((rotate_rows_kernel<false, true>), grid, dim3(256), kRingLds, stream, in, in_row_stride, rows,
+                       rop, out, out_row_stride);
+  else
+    hipLaunchKernelGGL((rotate_rows_kernel<false, false>), grid, dim3(256), kRingLds, stream, in, in_row_stride, rows,
+                       rop, out, out_row_stride);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 

@@ -4,7 +4,8 @@ Mirrors oscar_ascend/integration.py:17-44, 89-114: the KV-cache budget the
 engine may allocate is what remains after the fixed per-layer buffers, in
 whole cache blocks.  Per OSCAR layer the fixed buffers here are
   * R_k, R_v and their transposes, fp32       4 * D^2 * 4
-  * the two MFMA rotation operands             2 * oscar_rotation_operand_bytes(D)
+  * the MFMA rotation operands of R_k, R_v      3 * oscar_rotation_operand_bytes(D)
+    and R_v^T
   * the FP32 window arena                      rows * bs * (2 * Hk * D * 4 + 8)
   * its fp16 MFMA operand images (high and    rows * bs * 4 * Hk * D * 2
     low parts of K and of V)
@@ -47,7 +48,7 @@ def arena_rows(block_size: int, sink: int, recent: int, staging: int) -> int:
 
 def fixed_bytes_per_layer(head_dim: int, num_kv_heads: int, block_size: int, sink: int, recent: int,
                           staging: int, window: bool) -> int:
-    fixed = 4 * head_dim * head_dim * 4 + 2 * ROTATION_OPERAND_BYTES
+    fixed = 4 * head_dim * head_dim * 4 + 3 * ROTATION_OPERAND_BYTES
     if window:
         rows = arena_rows(block_size, sink, recent, staging)
         fixed += rows * block_size * (2 * num_kv_heads * head_dim * 4 + 4 * num_kv_heads * head_dim * 2 + 8 + 8) + 16
@@ -266,7 +267,7 @@ def install_runner_hooks() -> None:
             impl._set_caches(cache)
             k_cache = impl.key_cache
             impl._layer_rots(module, k_cache.device)
-            persistent += 4 * impl.head_size ** 2 * 4 + 2 * ROTATION_OPERAND_BYTES
+            persistent += 4 * impl.head_size ** 2 * 4 + 3 * ROTATION_OPERAND_BYTES
             if impl._oscar.window_enabled:
                 impl._ensure_staging(module, (impl.key_cache, impl.value_cache))
                 for attr in ("_oscar_stage_k", "_oscar_stage_v", "_oscar_slot_owner", "_oscar_seat_winner",

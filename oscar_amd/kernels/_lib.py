@@ -23,6 +23,7 @@ _c_i32, _c_i64, _c_sz, _c_p, _c_f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_s
 SIGNATURES = {
     "oscar_rotation_operand_bytes": (_c_sz, [_c_i32]),
     "oscar_rotation_operand": (_c_i32, [_c_p, _c_p, _c_i32, _c_p]),
+    "oscar_rotate_rows": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i64, _c_i32, _c_p, _c_p, _c_i32, _c_i64, _c_p]),
     "oscar_quant_write": (_c_i32, [_c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i64, _c_p, _c_p, _c_p,
                                    _c_p, _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                    _c_i64, _c_i64, _c_i32, _c_i32, _c_p]),

@@ -52,6 +52,31 @@ def rotation_operand(R: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def rotate_rows(x: torch.Tensor, operand: torch.Tensor, out_dtype=torch.float32, out=None) -> torch.Tensor:
+    """x @ R on MFMA for every D-feature row of x ([..., D], bf16 or fp32), R
+    given by its operand (rotation_operand); fp32 or bf16 result of x's shape,
+    written into `out` when given (a contiguous tensor of that shape).
+    Replaces the prefill route's fp32 rotations (backend.py:392-413)."""
+    D = x.shape[-1]
+    check_d(D)
+    if x.dtype not in (torch.bfloat16, torch.float32) or out_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("rotate_rows takes bf16 or fp32 rows and returns fp32 or bf16")
+    _check_device(x, operand)
+    rows = x.numel() // D
+    xr = x.reshape(rows, D)
+    if xr.stride(1) != 1 or xr.data_ptr() % 16 or (xr.stride(0) * xr.element_size()) % 16:
+        xr = xr.contiguous()
+    if out is None:
+        out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    if out.dtype != out_dtype or out.shape != x.shape or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor of x's shape and the output dtype")
+    orr = out.view(rows, D)
+    _lib.call("oscar_rotate_rows", _lib.ptr(xr), int(x.dtype == torch.float32), xr.stride(0), rows, D,
+              _lib.ptr(operand), _lib.ptr(orr), int(out_dtype == torch.bfloat16), orr.stride(0),
+              _lib.stream_handle(x.device))
+    return out
+
+
 def _token_rows(x: torch.Tensor, N: int, hk: int, D: int, dtype) -> tuple[torch.Tensor, int]:
     if x.dtype != dtype:
         raise ValueError(f"expected {dtype}, got {x.dtype}")
