@@ -278,12 +278,12 @@ struct StepLoad {
 // slot bytes), so the compiler can wait for exactly one step's loads while the
 // next step's are in flight; results that must not count are neutralised
 // where they are used.
-__device__ __forceinline__ StepLoad load_step(const DecodeArgs& a, const int (&pg)[kWaves], int tbase, int prefix,
-                                              int kvh, int w, int lane) {
+__device__ __forceinline__ StepLoad load_step(const DecodeArgs& a, const int (&pg)[kWaves], const int (&tb)[kWaves],
+                                              int prefix, int kvh, int w, int lane) {
   StepLoad L;
   const int t = lane & 31, g = lane >> 5;
   const int tq = lane & 7, bg = lane >> 3;
-  const int p0 = tbase + kTile * w;
+  const int p0 = w == 0 ? tb[0] : (w == 1 ? tb[1] : (w == 2 ? tb[2] : tb[3]));
   const int page = pg[w];
   const bool tile_ok = p0 < prefix && page >= 0;
   const int pgc = tile_ok ? page : 0;
@@ -311,7 +311,7 @@ __device__ __forceinline__ StepLoad load_step(const DecodeArgs& a, const int (&p
     const int tk = 64 * h + lane;
     const int j = tk >> 5;
     const int pj = j == 0 ? pg[0] : (j == 1 ? pg[1] : (j == 2 ? pg[2] : pg[3]));
-    const int pos = tbase + tk;
+    const int pos = (j == 0 ? tb[0] : (j == 1 ? tb[1] : (j == 2 ? tb[2] : tb[3]))) + (tk & (kTile - 1));
     const bool ok = arena && pj >= 0 && pos < prefix;
     const int64_t* op = ok ? a.owner + (int64_t)fast_mod((uint32_t)pj, a.rows_div) * a.block_size +
                                  fast_mod((uint32_t)pos, a.bs_div)
@@ -523,6 +523,20 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   const int kvh = it.kvh;
   const int nsplit = it.nsplit;
   const int nst = (steps - 1 - split) / nsplit + 1;     // steps split + nsplit k, k < nst (<= 64)
+  // Single-step launches with one split per step: wave j takes tile j of
+  // step (split + j * spread) mod nsplit, so that the four tiles of a step
+  // (the window steps, first and last, among them) go to four workgroups,
+  // whose waves then each hold at most one window tile's images.
+  const int spread = (!kMidIssue && nsplit == steps && nsplit >= 8) ? nsplit / 4 : 0;
+  auto step_of = [&](int k, int j) {
+    const int sj = split + j * spread;
+    return (sj >= nsplit ? sj - nsplit : sj) + nsplit * k;
+  };
+  // first token of tile j of the k-th step this workgroup takes
+  auto tile_bases = [&](int k, int (&tb)[kWaves]) {
+#pragma unroll
+    for (int j = 0; j < kWaves; ++j) tb[j] = step_of(k, j) * kStepTok + kTile * j;
+  };
   const bool arena = a.stage_rows > 0;
   // Positions whose staged value may replace the INT2 one: p < win_head or
   // p >= win_tail (every position for the MTP read).  Scalar loads, waited
@@ -556,7 +570,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
 #pragma unroll
   for (int j = 0; j < kWaves; ++j) {
     // token offsets stay below 2^31: (split + nsplit * lane) * 128 < 1024 * 64 * 128
-    const uint32_t tok0 = (uint32_t)(split + nsplit * lane) * kStepTok + kTile * j;
+    const uint32_t tok0 = (uint32_t)step_of(lane, j) * kStepTok + kTile * j;
     const uint32_t pidx = fast_div(tok0, a.bs_div);
     const bool ok = lane < nst && (int)tok0 < prefix && (int)pidx < a.bt_cols;
     const int p = bt_row[ok ? pidx : 0];
@@ -582,7 +596,9 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
     touched = *reinterpret_cast<const uint32_t*>(a.k_cache + pgk * a.k_page) ^
               *reinterpret_cast<const uint32_t*>(a.v_cache + pgk * a.v_page);
   }
-  StepLoad cur = load_step(a, pg, split * kStepTok, prefix, kvh, w, lane);
+  int tb0[kWaves];
+  tile_bases(0, tb0);
+  StepLoad cur = load_step(a, pg, tb0, prefix, kvh, w, lane);
 
   // ---- Q^T operand into LDS (permuted K dimension, fp16 high + low parts) and row sums ----
   // Thread: row r8, features 32 * c8 .. +31, which are exactly the four
@@ -629,14 +645,15 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
   const uint32_t ls0 = 8u - e2, rs0 = e2, ls1 = 4u - e2, rs1 = 4u + e2;
 
   auto run_step = [&](const StepLoad& L, int k, const int (&pgs)[kWaves], auto&& issue_next) {
-    const int tbase = (split + nsplit * k) * kStepTok;
+    int tb[kWaves];
+    tile_bases(k, tb);
     StepLds& B = S.buf[k & 1];
     // window-owned tokens of the step's four tiles (bit t of wmj: token t of tile j)
     uint32_t wm0 = 0u, wm1 = 0u, wm2 = 0u, wm3 = 0u;
     if (arena) {
       const int pa = g == 0 ? pgs[0] : pgs[1];
       const int pb = g == 0 ? pgs[2] : pgs[3];
-      const int q0 = tbase + lane, q1 = tbase + 64 + lane;
+      const int q0 = (g == 0 ? tb[0] : tb[1]) + col, q1 = (g == 0 ? tb[2] : tb[3]) + col;
       const bool s0 = pa >= 0 && q0 < prefix && (q0 < win_head || q0 >= win_tail) && L.own0 == pa;
       const bool s1 = pb >= 0 && q1 < prefix && (q1 < win_head || q1 >= win_tail) && L.own1 == pb;
       const uint64_t b0 = __ballot(s0), b1 = __ballot(s1);
@@ -647,7 +664,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
     }
     const uint32_t wmw = pick4(wm0, wm1, wm2, wm3, w);
     const int pgw = pick4(pgs[0], pgs[1], pgs[2], pgs[3], w);
-    const int p0 = tbase + kTile * w;
+    const int p0 = pick4(tb[0], tb[1], tb[2], tb[3], w);
     const int nvalid = pgw >= 0 ? min(kTile, max(prefix - p0, 0)) : 0;
     // A tile with window tokens reads the high part of their K operand image
     // now, a phase before the score pass uses it (the low part reuses these
@@ -778,7 +795,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
     const bool anywin = (wm0 | wm1 | wm2 | wm3) != 0u;
     auto vimg_of = [&](int j) {
       return reinterpret_cast<const half8*>(
-          a.vimg + image_index(a, pgs[j], (int)fast_mod((uint32_t)(tbase + kTile * j), a.bs_div), kvh) *
+          a.vimg + image_index(a, pgs[j], (int)fast_mod((uint32_t)tb[j], a.bs_div), kvh) *
                        kVImgHalfs);
     };
     half8 vim[kWaves][2][2];
@@ -880,10 +897,10 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
     // ---- O^T (features 64w .. 64w + 63) += V^T P'^T over the step's tiles ----
 #pragma unroll
     for (int j = 0; j < kWaves; ++j) {
-      if (pgs[j] < 0 || tbase + kTile * j >= prefix) continue;
+      if (pgs[j] < 0 || tb[j] >= prefix) continue;
       const uint32_t wmj = j == 0 ? wm0 : (j == 1 ? wm1 : (j == 2 ? wm2 : wm3));
       // a tile without INT2 tokens has all its P' zero: only its window part
-      const bool int2 = (tile_valid(min(kTile, prefix - (tbase + kTile * j))) & ~wmj) != 0u;
+      const bool int2 = (tile_valid(min(kTile, prefix - tb[j])) & ~wmj) != 0u;
       if (int2) {
         const uint32_t* vr = &B.vt[j][vrow * kVtRow];
         const _Float16* pr = &S.p[j][col * kPRow + 8 * g];
@@ -945,7 +962,9 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_kernel(DecodeArgs a
     StepLoad nxt;
     auto issue = [&] {
       step_pages(k + 1, pgn);
-      nxt = load_step(a, pgn, (split + nsplit * (k + 1)) * kStepTok, prefix, kvh, w, lane);
+      int tbn[kWaves];
+      tile_bases(k + 1, tbn);
+      nxt = load_step(a, pgn, tbn, prefix, kvh, w, lane);
     };
     if constexpr (kMidIssue) {
       run_step(cur, k, pg, issue);
