@@ -1198,7 +1198,14 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(Decode
   const int c = lane & 15, G = lane >> 4, t32 = lane & 31;
   const int kvh = it.kvh;
   const int nsplit = it.nsplit;
-  const int nst = (steps - 1 - split) / nsplit + 1;
+  // Wave w walks the steps of split (split + w * nsplit / 4) mod nsplit (for
+  // items of at least 8 splits, none of them empty), so that the tiles of
+  // one step (a window step's among them) go to four workgroups and no CU
+  // loads more than one window tile's images per step; the waves are
+  // independent, so their tile counts may differ by one.
+  const int sw0 = split + ((nsplit >= 8 && nsplit <= steps) ? w * (nsplit / 4) : 0);
+  const int sw = sw0 >= nsplit ? sw0 - nsplit : sw0;
+  const int nst = (steps - 1 - sw) / nsplit + 1;
   const bool arena = a.stage_rows > 0;
   int win_head = 0, win_tail = 0;
   if (a.win) {
@@ -1226,7 +1233,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(Decode
   int pgv;
   {
     const int32_t* bt_row = a.block_table + (int64_t)it.req * a.bt_stride;
-    const uint32_t tok0 = (uint32_t)(split + nsplit * lane) * kStepTok + kTile * w;
+    const uint32_t tok0 = (uint32_t)(sw + nsplit * lane) * kStepTok + kTile * w;
     const uint32_t pidx = fast_div(tok0, a.bs_div);
     const bool ok = lane < nst && (int)tok0 < prefix && (int)pidx < a.bt_cols;
     const int p = bt_row[ok ? pidx : 0];
@@ -1236,7 +1243,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_split_small_kernel(Decode
     const int p = __builtin_amdgcn_readlane(pgv, k);
     return (p >= 0 && p < a.num_pages) ? p : -1;
   };
-  auto tile_pos = [&](int k) { return (split + nsplit * k) * kStepTok + kTile * w; };
+  auto tile_pos = [&](int k) { return (sw + nsplit * k) * kStepTok + kTile * w; };
   // Processing order: the wavefront's last tile first (the one that holds the
   // recent window when any does, so its window pass can run while the next
   // tiles are in flight), then tiles 0, 1, ...; ring slot i % kSmRing holds the
