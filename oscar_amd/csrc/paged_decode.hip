@@ -2105,22 +2105,49 @@ bool plan_splits(DecodeArgs& a, unsigned nitems, int64_t max_history, int tiles_
     total += steps[i];
     max_steps = steps[i] > max_steps ? steps[i] : max_steps;
   }
+  // Automatic: the common number T of steps per split, the smallest that
+  // keeps the history splits within one round of resident workgroups.  An
+  // item whose last step holds at most one tile's tokens may leave that step
+  // out of the count when that lowers T (its split then takes T steps and
+  // the short one): 8 DecodeOnly reads of 32769 positions (257 steps) take
+  // 4 steps per split over 512 workgroups instead of 5 over 416.
+  int64_t counted[kMaxInlineItems];
+  int64_t total_cut = 0;
+  for (unsigned i = 0; i < nitems; ++i) {
+    const int64_t r = (int64_t)a.items[i].prefix % kStepTok;
+    counted[i] = steps[i] - ((steps[i] > 1 && r != 0 && r <= kTile) ? 1 : 0);
+    total_cut += counted[i];
+  }
+  auto least_t = [&](const int64_t* cnt, int64_t sum) {
+    int64_t t = (sum + kResidentSplitWgs - 1) / kResidentSplitWgs;
+    for (t = t < 1 ? 1 : t;; ++t) {
+      int64_t n = 0;
+      for (unsigned i = 0; i < nitems; ++i) n += (cnt[i] + t - 1) / t;
+      if (n <= kResidentSplitWgs || t >= kMaxStepsPerSplit) return t;
+    }
+  };
   int64_t T = 0, S = 0;
+  const int64_t* cnt = steps;
   if (tiles_per_split > 0) {
     S = splits_for(max_history, tiles_per_split);
   } else {
-    T = (total + kResidentSplitWgs - 1) / kResidentSplitWgs;
-    T = T < 1 ? 1 : T;
-    for (;; ++T) {
-      int64_t n = 0;
-      for (unsigned i = 0; i < nitems; ++i) n += (steps[i] + T - 1) / T;
-      if (n <= kResidentSplitWgs || T >= kMaxStepsPerSplit) break;
+    T = least_t(steps, total);
+    const int64_t Tc = least_t(counted, total_cut);
+    if (Tc < T) {
+      T = Tc;
+      cnt = counted;
     }
   }
   int64_t slots = 0, max_split = 0;
+  bool empty = false;
   for (unsigned i = 0; i < nitems; ++i) {
-    int64_t n = tiles_per_split > 0 ? S : (steps[i] + T - 1) / T;
+    int64_t n = tiles_per_split > 0 ? S : (cnt[i] + T - 1) / T;
+    if (tiles_per_split == 0) {
+      const int64_t lo = (steps[i] + kMaxStepsPerSplit - 1) / kMaxStepsPerSplit;   // one page lane per step
+      n = n > lo ? n : lo;
+    }
     n = n < steps[i] ? n : steps[i];
+    empty = empty || (n == 0 && a.items[i].nq > 0);
     if (n > kMaxSplits) return false;
     a.items[i].nsplit = (int16_t)n;
     a.items[i].pbase = (int32_t)slots;
@@ -2128,7 +2155,8 @@ bool plan_splits(DecodeArgs& a, unsigned nitems, int64_t max_history, int tiles_
     max_split = n > max_split ? n : max_split;
   }
   a.max_splits = (int32_t)max_split;
-  a.fresh_block = fresh && slots <= kResidentSplitWgs ? 1 : 0;
+  // (a request without history has no split to carry its fresh partial)
+  a.fresh_block = fresh && (slots <= kResidentSplitWgs || empty) ? 1 : 0;
   a.nitems = (int32_t)nitems;
   return true;
 }

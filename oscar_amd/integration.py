@@ -88,16 +88,25 @@ def decode_split_plan(query_lens, histories, max_history: int, tiles_per_split: 
     Explicit tiles per split: ceil(tiles / tps) splits per item.  Automatic:
     the smallest common number T of 128-token steps per split (T <= 64) that
     keeps the history splits within one round of resident workgroups, and
-    ceil(steps / T) splits per item; never more splits than steps."""
+    ceil(steps / T) splits per item, where a last step of at most one tile
+    (32 tokens) goes uncounted when that lowers T; never more splits than
+    steps."""
     steps = [-(-h // DECODE_STEP) if q > 0 and h > 0 else 0 for q, h in zip(query_lens, histories)]
     if tiles_per_split:
         tiles = -(-max_history // DECODE_TILE) if max_history > 0 else 0
         per = [-(-tiles // tiles_per_split)] * len(steps)
     else:
-        T = max(1, -(-sum(steps) // DECODE_RESIDENT_SPLITS))
-        while sum(-(-n // T) for n in steps) > DECODE_RESIDENT_SPLITS and T < DECODE_MAX_STEPS_PER_SPLIT:
-            T += 1
-        per = [-(-n // T) for n in steps]
+        def least_t(cnt):
+            t = max(1, -(-sum(cnt) // DECODE_RESIDENT_SPLITS))
+            while sum(-(-n // t) for n in cnt) > DECODE_RESIDENT_SPLITS and t < DECODE_MAX_STEPS_PER_SPLIT:
+                t += 1
+            return t
+        # a last step of at most one tile's tokens may go uncounted when that lowers T
+        cut = [s - (1 if s > 1 and 0 < h % DECODE_STEP <= DECODE_TILE else 0) for s, h in zip(steps, histories)]
+        T, Tc = least_t(steps), least_t(cut)
+        cnt = cut if Tc < T else steps
+        T = min(T, Tc)
+        per = [max(-(-n // T), -(-s // DECODE_MAX_STEPS_PER_SPLIT)) for n, s in zip(cnt, steps)]
     nsplit, pbase, slot = [], [], 0
     for n, st in zip(per, steps):
         n = min(n, st)

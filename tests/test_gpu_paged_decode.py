@@ -86,6 +86,17 @@ def test_more_requests_than_one_launch_carries(device):
     run_case(case, device)
 
 
+def test_request_without_history_among_many_splits(device):
+    """127 requests of 4 steps, a split each (635 partial slots, more than one
+    round of resident workgroups), and one request whose only keys are its own
+    new tokens: it has no history split to carry its fresh partial, so the
+    launch gives every fresh partial a workgroup of its own."""
+    hist = [512] * 64 + [0] + [512] * 63
+    case = decode_case(hist, [4] * 64 + [2] + [4] * 63, bs=128, seed=14, pool_pages=700, sink=128, recent=128,
+                       staging=256)
+    run_case(case, device)
+
+
 def test_window_disabled_matches_pure_int2(device):
     case = decode_case([3000], [4], seed=8, window=False)
     run_case(case, device, with_stage=False)
