@@ -499,3 +499,37 @@ def test_bench_profile_figures_need_unchanged_sources(tmp_path, monkeypatch):
     (src / "k.hip").write_text("kernel v2\n")
     assert bench.profile_figures("t.txt") == {}
     assert bench.profile_figures("missing.txt") == {}
+
+
+@pytest.mark.parametrize("q_lens,hist", [
+    ([4], [24579]),                                          # one request, one step per split
+    ([1] * 8, [32768] * 8),                                  # 8 x 256 steps: 4 steps per split, 512 splits
+    ([4] * 32, [2048 + 448 * i for i in range(32)]),         # mixed lengths
+    ([1] * 3, [300000, 5, 0]),                               # a long request, a tiny one and an empty one
+])
+def test_decode_split_plan_invariants(q_lens, hist):
+    """Restated split plan (paged_decode.hip plan_splits): every split takes
+    at most 64 steps (one page-register lane each), no item gets more splits
+    than steps, the history splits stay within one round of resident
+    workgroups when 64 steps per split allow it, and the partial slots fit the
+    workspace bound."""
+    nsplit, pbase = integration.decode_split_plan(q_lens, hist, max(hist))
+    steps = [-(-h // integration.DECODE_STEP) for h in hist]
+    for n, s in zip(nsplit, steps):
+        assert n <= s
+        if s:
+            assert n >= 1 and -(-s // n) <= integration.DECODE_MAX_STEPS_PER_SPLIT
+    if sum(-(-s // integration.DECODE_MAX_STEPS_PER_SPLIT) for s in steps) <= integration.DECODE_RESIDENT_SPLITS:
+        assert sum(nsplit) <= integration.DECODE_RESIDENT_SPLITS
+    assert pbase[-1] + nsplit[-1] + 1 <= integration.decode_partial_slots(len(hist), max(hist))
+
+
+def test_decode_split_plan_leaves_a_one_tile_last_step_uncounted():
+    """8 DecodeOnly reads of 32769 positions: 257 steps, the last holding one
+    token.  Counting it would need 5 steps per split (52 splits per item);
+    leaving it out gives 64 splits of 4 steps (split 0 also takes the short
+    step), 512 workgroups in all.  A last step of 33 tokens is counted."""
+    nsplit, _ = integration.decode_split_plan([1] * 8, [32769] * 8, 32769, fresh=0)
+    assert nsplit == [64] * 8
+    nsplit, _ = integration.decode_split_plan([1] * 8, [32768 + 33] * 8, 32768 + 33, fresh=0)
+    assert nsplit == [52] * 8
