@@ -393,27 +393,11 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// Workgroups [stagger_lo, stagger_hi) start about 10 us late.  On MI355X
-// the dispatcher gives CU c of each XCD the workgroups c and c + #CUs first,
-// in the same phase (rotation on MFMA, then the selection on VALU); holding
-// back the second one for about half a workgroup's run lets one's selection
-// overlap the other's rotation, and the offset carries into later rounds
-// (measured: C5 write 77 -> 69 us).
-constexpr int kStaggerSleeps = 3;     // s_sleep 127 = 8128 clocks each
-
 __global__ __launch_bounds__(256, 2) void quant_write_fused_kernel(
     const uint16_t* __restrict__ key, const uint16_t* __restrict__ value, int64_t n_tokens,
     int64_t token_stride, const uint8_t* __restrict__ rot_k, const uint8_t* __restrict__ rot_v,
-    const int64_t* __restrict__ slots, CacheArgs c, int clip_k, int clip_v, int stagger_lo, int stagger_hi,
-    WindowArgs w) {
+    const int64_t* __restrict__ slots, CacheArgs c, int clip_k, int clip_v, WindowArgs w) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring[];     // ring, then the selection buffers
-  {
-    const int lin = blockIdx.x + gridDim.x * blockIdx.y;
-    if (lin >= stagger_lo && lin < stagger_hi) {
-#pragma unroll 1
-      for (int i = 0; i < kStaggerSleeps; ++i) __builtin_amdgcn_s_sleep(127);
-    }
-  }
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -842,17 +826,6 @@ int quant_write_impl(const void* key_bf16, const void* value_bf16, int64_t num_t
   if (set_dynamic_lds(reinterpret_cast<const void*>(quant_write_fused_kernel), (int)kFusedLds, g_lds_set) != kOk) return kErrLaunch;
   const int64_t per_block = kFusedWaves * kTokPerWave;
   dim3 grid((unsigned)((num_tokens + per_block - 1) / per_block), (unsigned)(num_kv_heads * 2));
-  // The second workgroup of each CU is held back when the grid fills the GPU
-  // at least twice over (two resident per CU) and a clip threshold is searched
-  // (the VALU phase the other workgroup's rotation overlaps).
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return kErrLaunch;
-  const int64_t blocks = (int64_t)grid.x * grid.y;
-  const bool stagger = blocks >= 4 * (int64_t)cus && (clip_index_k >= 0 || clip_index_v >= 0);
-  const int lo = stagger ? cus : 0;
-  const int hi = stagger ? 2 * cus : 0;
   if (w.rows > 0) {
     hipLaunchKernelGGL(quant_window_winner_kernel, dim3((unsigned)((num_tokens + 255) / 256)), dim3(256), 0, stream,
                        slot_mapping, (int32_t)num_tokens, w.winner, block_size, w.rows);
@@ -862,7 +835,7 @@ int quant_write_impl(const void* key_bf16, const void* value_bf16, int64_t num_t
                      static_cast<const uint16_t*>(key_bf16), static_cast<const uint16_t*>(value_bf16),
                      num_tokens, token_stride, static_cast<const uint8_t*>(rot_k_operand),
                      static_cast<const uint8_t*>(rot_v_operand), slot_mapping, c,
-                     (int)clip_index_k, (int)clip_index_v, lo, hi, w);
+                     (int)clip_index_k, (int)clip_index_v, w);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
